@@ -1,0 +1,241 @@
+#!/usr/bin/env python3
+"""RPA benchmark on one MI355X.
+
+Default workload: BASELINE config 2, the Llama-3-8B-shape decode batch
+(64 sequences x 1 query token, 32 q / 8 kv heads, head_dim 128, page_size 16,
+bf16 KV, kv_lens ~ U[512, 4096], 20k-page shuffled pool).  One "step" is one
+full ragged_paged_attention call (cache write + attention) over that batch with
+every input already resident in HBM.
+
+Prints one JSON line:
+  value      -- query tokens per second of whole calls (HIP-graph replay of the
+                call, so host launch overhead is not on the clock; the eager
+                figure is reported beside it)
+  roofline   -- the attention kernel's algorithmic HBM bytes per launch divided
+                by its average launch duration (HIP events around a graph of
+                attention-only launches on the launching stream), against
+                MI355X's 8 TB/s
+  cpu_baseline -- the CPU oracle (faithful restatement of the reference
+                ref_ragged_paged_attention) on the host cores, same workload
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--config 2]
+"""
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBPS = 8000.0
+BF16_PEAK_TFLOPS = 2500.0
+
+WORKLOAD_TEXT = {
+    1: "C1 CPU-reference decode: 4 seqs x 1 token, 8q/2kv, D128, ps16, bf16, kv~U[64,512]",
+    2: "C2 Llama-3-8B-shape decode batch: 64 seqs x 1 token, 32q/8kv, D128, ps16, bf16 KV, "
+       "kv_lens~U[512,4096], 20k-page pool",
+    3: "C3 mixed: 8x512-token prefill chunks (ctx~U[0,4096]) + 120 decodes (kv~U[1024,8192]), "
+       "64q/8kv, D128, ps32, bf16",
+    4: "C4 long-context fp8: 16 decodes kv~U[16384,32768], 32q/8kv, D128, ps64, fp8-e4m3 KV",
+    5: "C5 Gemma-style: 16 decodes + 16x256 chunks, 16q/8kv, D256, ps16, window 4096, cap 50",
+}
+
+
+def _log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def cpu_baseline(w, seconds):
+    """Time the CPU oracle (faithful mode) on the same workload."""
+    import torch
+
+    from oracle import rpa_oracle as O
+
+    threads = os.cpu_count() or 1
+    torch.set_num_threads(threads)
+    model = "unknown"
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    O.ref_ragged_paged_attention(*w.args(), mode="faithful", validate=False, **w.kwargs)
+    times = []
+    t_start = time.perf_counter()
+    while len(times) < 5 and (time.perf_counter() - t_start < seconds or len(times) < 1):
+        t0 = time.perf_counter()
+        O.ref_ragged_paged_attention(*w.args(), mode="faithful", validate=False, **w.kwargs)
+        times.append(time.perf_counter() - t0)
+    med = statistics.median(times)
+    return {
+        "value": w.num_tokens / med,
+        "unit": "tokens/s",
+        "cores": torch.get_num_threads(),
+        "kind": "port",
+        "sample": (f"full workload ({w.num_seqs} seqs, {w.num_tokens} query tokens) per call; "
+                   f"median of {len(times)} calls after 1 warm-up; {med * 1e3:.1f} ms/call; "
+                   f"oracle faithful mode (torch CPU) on {model}"),
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--config", type=int, default=2, choices=[1, 2, 3, 4, 5])
+    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-graph", action="store_true")
+    args = ap.parse_args()
+
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(f"bench.py measures one GPU only (got --gpus {args.gpus}, WORLD_SIZE={world}): "
+              "RPA shards by KV heads / sequences with no exchange inside attention, so a "
+              "single MI355X's throughput is the measured figure; multi-GPU runs are not part "
+              "of this build.", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    import vllm_torchtpu_amd as R
+    import vllm_torchtpu_amd.workloads as W
+    from vllm_torchtpu_amd.util import cdiv
+
+    dev = torch.device("cuda:0")
+    _log(f"building workload C{args.config}")
+    w = W.baseline_config(args.config)
+    g = w.to(dev)
+    kw = dict(w.kwargs)
+    torch.cuda.synchronize()
+
+    def step():
+        return R.ragged_paged_attention(*g.args(), **kw)
+
+    def attn_only():
+        return R.ragged_paged_attention(*g.args(), skip_kv_update=True, **kw)
+
+    _log("warm-up")
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+
+    # Eager: K whole calls back to back.
+    _log(f"timing {args.steps} eager steps")
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    eager_s = time.perf_counter() - t0
+
+    graph_s = None
+    attn_ms = None
+    if not args.no_graph:
+        _log("capturing HIP graphs")
+        s = torch.cuda.Stream(dev)
+        s.wait_stream(torch.cuda.current_stream(dev))
+        with torch.cuda.stream(s):
+            for _ in range(2):
+                step()
+                attn_only()
+        torch.cuda.current_stream(dev).wait_stream(s)
+        torch.cuda.synchronize()
+        g_step = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g_step):
+            step()
+        g_attn = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g_attn):
+            attn_only()
+        for _ in range(3):
+            g_step.replay()
+            g_attn.replay()
+        torch.cuda.synchronize()
+        _log(f"timing {args.steps} graph steps")
+        t0 = time.perf_counter()
+        for _ in range(args.steps):
+            g_step.replay()
+        torch.cuda.synchronize()
+        graph_s = time.perf_counter() - t0
+        # Attention kernel alone, HIP events on the replay stream.
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(args.steps):
+            g_attn.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        attn_ms = e0.elapsed_time(e1) / args.steps
+
+    timed_s = graph_s if graph_s is not None else eager_s
+    tokens = w.num_tokens
+    value = tokens * args.steps / timed_s
+    ms_per_step = timed_s / args.steps * 1e3
+
+    from oracle import rpa_oracle as O  # byte/flop formulas only
+
+    kvl = w.kv_lens.tolist()
+    cu = w.cu_q_lens.tolist()
+    n = w.num_seqs
+    hq, hkv, d = w.q.shape[1], w.k.shape[1], w.q.shape[2]
+    dp = w.kv_cache.shape[4]
+    ps = w.kv_cache.shape[1]
+    kvb = w.kv_cache.element_size()
+    qb = w.q.element_size()
+    win = kw.get("sliding_window")
+    call_bytes = O.algorithmic_bytes(kvl, cu, n, hq, hkv, d, dp, ps, qb, kvb, qb,
+                                     sliding_window=win)
+    # Attention-only launch: no new-KV write.
+    newkv = sum((cu[i + 1] - cu[i]) * 2 * hkv * dp * kvb for i in range(n))
+    attn_bytes = call_bytes - newkv
+    flops = O.algorithmic_flops(kvl, cu, n, hq, d, sliding_window=win)
+
+    roofline = None
+    if attn_ms is not None:
+        achieved = attn_bytes / (attn_ms * 1e-3) / 1e9
+        roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS,
+                    "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4),
+                    "traffic": None, "kernel_ms": round(attn_ms, 5),
+                    "bytes_per_launch": attn_bytes}
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        _log("timing CPU oracle baseline")
+        cpu = cpu_baseline(w, args.cpu_seconds)
+
+    line = {
+        "metric": "RPA tokens/s + achieved HBM GB/s (% of 8 TB/s), Llama-3-8B-shape decode batch",
+        "value": round(value, 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16" if kvb == 2 else ("fp8-e4m3 KV / bf16 q" if kvb == 1 else "f32"),
+        "data": "synthetic (seeded N(0,1) Q/K/V, shuffled page pool)",
+        "config": {"workload": WORKLOAD_TEXT[args.config], "num_seqs": n,
+                   "query_tokens": tokens, "kv_tokens": int(sum(kvl[:n])),
+                   "parallelism": "single GPU"},
+        "call_bytes": call_bytes,
+        "call_gbps": round(call_bytes / (ms_per_step * 1e-3) / 1e9, 1),
+        "eager_tokens_per_s": round(tokens * args.steps / eager_s, 1),
+        "eager_ms_per_step": round(eager_s / args.steps * 1e3, 5),
+        "prefill_flops": flops,
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,89 @@
+"""Shared helpers for the RPA tests: an independent brute-force reference and
+comparison utilities.  Test infrastructure only."""
+
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import torch
+
+
+def brute_force_rpa(q, k, v, kv_cache, kv_lens, page_indices, cu_q_lens, distribution, *,
+                    sm_scale=1.0, sliding_window=None, soft_cap=None, k_scale=None,
+                    v_scale=None, use_causal_mask=True, skip_kv_update=False):
+    """Per-element fp64 attention written directly from the semantic contract
+    (positions, page table, K/V combined-head interleave), independent of the
+    oracle's gather/einsum code.  Returns [num_tokens, Hq, D] float64."""
+    Q = q.to(torch.float64).numpy()
+    K = k.to(torch.float64).numpy()
+    V = v.to(torch.float64).numpy()
+    C = kv_cache.to(torch.float64).numpy()
+    _, ps, _, pack, _ = kv_cache.shape
+    T, Hq, D = q.shape
+    Hkv = k.shape[1]
+    qpk = Hq // Hkv
+    S = kv_lens.shape[0]
+    pps = page_indices.shape[0] // S
+    n = int(distribution[2])
+    cu = [int(x) for x in cu_q_lens.tolist()]
+    kvl = [int(x) for x in kv_lens.tolist()]
+    pt = [int(x) for x in page_indices.tolist()]
+    out = np.zeros((cu[n], Hq, D))
+    for s in range(n):
+        q0, ql, kl = cu[s], cu[s + 1] - cu[s], kvl[s]
+        for i in range(ql):
+            pos = kl - ql + i
+            for gq in range(Hq):
+                h = gq // qpk
+                logits, vals = [], []
+                for j in range(kl):
+                    if skip_kv_update or j < kl - ql:
+                        page, slot = pt[s * pps + j // ps], j % ps
+                        kr = C[page, slot, (2 * h) // pack, (2 * h) % pack, :D]
+                        vr = C[page, slot, (2 * h + 1) // pack, (2 * h + 1) % pack, :D]
+                    else:
+                        t = q0 + j - (kl - ql)
+                        kr, vr = K[t, h], V[t, h]
+                    if use_causal_mask:
+                        if j > pos:
+                            continue
+                        if sliding_window is not None and j <= pos - sliding_window:
+                            continue
+                    x = float(np.dot(Q[q0 + i, gq], kr)) * sm_scale
+                    if k_scale is not None:
+                        x *= k_scale
+                    if soft_cap is not None:
+                        x = soft_cap * math.tanh(x / soft_cap)
+                    logits.append(x)
+                    vals.append(vr)
+                m = max(logits)
+                w = [math.exp(x - m) for x in logits]
+                tot = sum(w)
+                o = sum(wi * vi for wi, vi in zip(w, vals)) / tot
+                if v_scale is not None:
+                    o = o * v_scale
+                out[q0 + i, gq] = o
+    return torch.from_numpy(out)
+
+
+def assert_close(actual, expected, atol, rtol, what=""):
+    a = actual.to(torch.float64).cpu()
+    e = expected.to(torch.float64).cpu()
+    assert a.shape == e.shape, (a.shape, e.shape)
+    err = (a - e).abs()
+    bound = atol + rtol * e.abs()
+    bad = err > bound
+    if bad.any():
+        idx = bad.nonzero()[0].tolist()
+        raise AssertionError(
+            f"{what}: {int(bad.sum())}/{bad.numel()} elements out of tolerance "
+            f"(atol={atol}, rtol={rtol}); max err {err.max().item():.4g}; first bad {idx}: "
+            f"actual {a[tuple(idx)].item():.6g} expected {e[tuple(idx)].item():.6g}")
+
+
+def bytes_equal(a: torch.Tensor, b: torch.Tensor) -> bool:
+    """Bitwise equality of two tensors of the same dtype (NaN-safe)."""
+    assert a.dtype == b.dtype and a.shape == b.shape
+    itype = {1: torch.uint8, 2: torch.int16, 4: torch.int32, 8: torch.int64}[a.element_size()]
+    return bool(torch.equal(a.contiguous().view(itype).cpu(), b.contiguous().view(itype).cpu()))

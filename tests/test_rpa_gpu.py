@@ -1,0 +1,252 @@
+"""GPU parity tests: the HIP library (through its C ABI, via the Python API)
+against the CPU oracle on identical seeded inputs.
+
+Bars: the cache write is bit exact; outputs are within atol = rtol = 2e-2
+(bf16 KV) or 5e-2 (fp8 KV) of the oracle's fp32-accumulation mode.  Case lists
+follow the reference's tests (tests/kernels/experimental/batched_rpa/
+correctness_test.py:472-986, tests/kernels/test_rpa_skip_kv_update.py:98-182,
+tests/kernels/test_rpa_bundled.py:58-227).
+"""
+
+import sys
+
+import pytest
+import torch
+
+from oracle import rpa_oracle as O
+from rpa_testlib import assert_close, bytes_equal
+
+import vllm_torchtpu_amd as R
+import vllm_torchtpu_amd.workloads as W
+from vllm_torchtpu_amd import _native as N
+
+pytestmark = pytest.mark.gpu
+
+BF16, E4M3, E5M2 = torch.bfloat16, torch.float8_e4m3fn, torch.float8_e5m2
+TOL = {BF16: 2e-2, E4M3: 5e-2, E5M2: 5e-2, torch.float32: 2e-2}
+
+
+def _log(msg):
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+def run_gpu(w, dev, path=N.RPA_PATH_AUTO, **extra):
+    g = w.to(dev)
+    kw = dict(w.kwargs)
+    kw.update(extra)
+    if path == N.RPA_PATH_AUTO:
+        out, cache = R.ragged_paged_attention(*g.args(), **kw)
+    else:
+        out = torch.empty(g.q.shape, dtype=g.q.dtype, device=dev)
+        q = g.q
+        R.rpa._rpa_forward_impl(q, g.k, g.v, g.kv_cache, g.kv_lens, g.page_indices,
+                                g.cu_q_lens, g.distribution, out,
+                                use_causal_mask=kw.get("use_causal_mask", True),
+                                skip_kv_update=kw.get("skip_kv_update", False),
+                                sm_scale=kw["sm_scale"],
+                                sliding_window=kw.get("sliding_window"),
+                                soft_cap=kw.get("soft_cap"), q_scale=kw.get("q_scale"),
+                                k_scale=kw.get("k_scale"), v_scale=kw.get("v_scale"),
+                                path=path)
+        cache = g.kv_cache
+    torch.cuda.synchronize()
+    return out[:w.num_tokens].cpu(), cache.cpu()
+
+
+def check(w, dev, path=N.RPA_PATH_AUTO, **extra):
+    _log(f"[rpa-gpu] case {w.name} seqs={w.seq_lens[:6]}{'...' if len(w.seq_lens) > 6 else ''}"
+         f" q={tuple(w.q.shape)} cache={tuple(w.kv_cache.shape)} {w.kv_cache.dtype} path={path}"
+         f" kw={ {k: v for k, v in {**w.kwargs, **extra}.items() if k != 'sm_scale'} }")
+    kw = dict(w.kwargs)
+    kw.update(extra)
+    exp_out, exp_cache = O.ref_ragged_paged_attention(*w.args(), mode="fp32", **kw)
+    out, cache = run_gpu(w, dev, path, **extra)
+    tol = TOL[w.kv_cache.dtype]
+    assert_close(out, exp_out, tol, tol, f"{w.name} output")
+    assert bytes_equal(cache, exp_cache), f"{w.name}: cache differs from the oracle"
+    return out
+
+
+# ---------------------------------------------------------------------------
+# cache write
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("dt", [BF16, E4M3, torch.float32])
+@pytest.mark.parametrize("d", [128, 80])
+def test_kv_cache_update_bit_exact(gpu_device, dt, d):
+    w = W.make_workload([(5, 18), (1, 33), (16, 48), (3, 3), (1, 1)], 8, 2, d, 16,
+                        kv_dtype=dt, seed=21, max_num_seqs=7, max_num_tokens=40,
+                        k_scale=0.5 if dt == E4M3 else None, v_scale=0.5 if dt == E4M3 else None)
+    _log(f"[rpa-gpu] kv update {dt} d={d}")
+    expect = O.update_kv_cache_np(w.k, w.v, w.kv_cache, w.kv_lens, w.page_indices,
+                                  w.cu_q_lens, w.distribution)
+    g = w.to(gpu_device)
+    R.rpa_kv_cache_update(g.k, g.v, g.kv_cache, g.kv_lens, g.page_indices, g.cu_q_lens,
+                          g.distribution)
+    torch.cuda.synchronize()
+    assert bytes_equal(g.kv_cache.cpu(), expect)
+
+
+def test_kv_cache_update_nan_payloads(gpu_device):
+    """NaN and -0.0 in new K/V are copied as bits."""
+    w = W.make_workload([(4, 20)], 4, 2, 128, 16, seed=22)
+    w.k[0, 0, :4] = torch.tensor([float("nan"), -0.0, float("inf"), -float("inf")])
+    expect = O.update_kv_cache_np(w.k, w.v, w.kv_cache, w.kv_lens, w.page_indices,
+                                  w.cu_q_lens, w.distribution)
+    g = w.to(gpu_device)
+    R.rpa_kv_cache_update(g.k, g.v, g.kv_cache, g.kv_lens, g.page_indices, g.cu_q_lens,
+                          g.distribution)
+    torch.cuda.synchronize()
+    assert bytes_equal(g.kv_cache.cpu(), expect)
+
+
+# ---------------------------------------------------------------------------
+# attention: reference case lists
+# ---------------------------------------------------------------------------
+BASIC = [(192, 328), (128, 180), (64, 255)]
+DECODE16 = [(1, k) for k in (18, 129, 597, 122, 64, 322, 463, 181, 1107, 123, 31, 18, 1229,
+                             229, 87, 1328)]
+PREFILL16 = [(5, 18), (15, 129), (120, 597), (100, 122), (21, 64), (32, 322), (251, 463),
+             (40, 181), (64, 1107), (99, 123), (10, 31), (5, 18), (3, 1229), (120, 229),
+             (9, 87), (2, 1328)]
+MIXED16 = [(5, 18), (1, 129), (120, 597), (1, 122), (1, 64), (32, 322), (251, 463), (1, 181),
+           (1, 1107), (99, 123), (1, 31), (5, 18), (3, 1229), (117, 229), (1, 87), (1, 1328)]
+
+PATHS = [N.RPA_PATH_AUTO, N.RPA_PATH_GENERIC]
+
+
+@pytest.mark.parametrize("path", PATHS)
+@pytest.mark.parametrize("ps", [16, 32])
+def test_basic(gpu_device, path, ps):
+    check(W.make_workload(BASIC, 32, 8, 128, ps, seed=1234, name="basic"), gpu_device, path)
+
+
+@pytest.mark.parametrize("path", PATHS)
+@pytest.mark.parametrize("name,seqs", [("decode", DECODE16), ("prefill", PREFILL16),
+                                       ("mixed", MIXED16)])
+def test_segments(gpu_device, path, name, seqs):
+    n = len(seqs)
+    dist = [n, n, n] if name == "decode" else [0, 0, n]
+    check(W.make_workload(seqs, 32, 8, 128, 16, seed=1234, distribution=dist, name=name),
+          gpu_device, path)
+
+
+@pytest.mark.parametrize("num_seqs", [1, 17])
+@pytest.mark.parametrize("heads", [(32, 8), (12, 2), (5, 1), (3, 3)])
+@pytest.mark.parametrize("d", [80, 240])
+def test_complex_shapes(gpu_device, num_seqs, heads, d):
+    g = torch.Generator().manual_seed(1234)
+    ql = torch.randint(1, 100, (num_seqs,), generator=g)
+    kl = ql + torch.randint(0, 50, (num_seqs,), generator=g)
+    seqs = list(zip(ql.tolist(), kl.tolist()))
+    check(W.make_workload(seqs, heads[0], heads[1], d, 16, seed=5, name="complex"), gpu_device)
+
+
+@pytest.mark.parametrize("window", [None, 5, 128])
+def test_sliding_window(gpu_device, window):
+    g = torch.Generator().manual_seed(1234)
+    ql = torch.randint(1, 100, (5,), generator=g)
+    kl = ql + torch.randint(0, 50, (5,), generator=g)
+    check(W.make_workload(list(zip(ql.tolist(), kl.tolist())), 4, 4, 128, 16, seed=6,
+                          sliding_window=window, name="window"), gpu_device)
+
+
+@pytest.mark.parametrize("cap", [None, 50.0, 2.0])
+def test_soft_cap(gpu_device, cap):
+    g = torch.Generator().manual_seed(1234)
+    ql = torch.randint(1, 100, (2,), generator=g)
+    kl = ql + torch.randint(0, 50, (2,), generator=g)
+    w = W.make_workload(list(zip(ql.tolist(), kl.tolist())), 16, 2, 128, 16, seed=7,
+                        soft_cap=cap, name="softcap")
+    w.q.mul_(4.0)  # push logits into the capped range
+    check(w, gpu_device)
+
+
+@pytest.mark.parametrize("dt", [E4M3, E5M2])
+@pytest.mark.parametrize("scales", [(0.5, 0.5), (None, None), (1.7, 0.6)])
+def test_fp8_kv(gpu_device, dt, scales):
+    check(W.make_workload(BASIC, 32, 8, 128, 16, kv_dtype=dt, seed=1234, k_scale=scales[0],
+                          v_scale=scales[1], name="fp8"), gpu_device)
+
+
+@pytest.mark.parametrize("dt", [E4M3, E5M2])
+def test_q_scale(gpu_device, dt):
+    check(W.make_workload(BASIC, 32, 8, 128, 16, kv_dtype=dt, seed=1234, k_scale=0.5,
+                          v_scale=0.5, q_scale=0.5, name="q_scale"), gpu_device)
+
+
+def test_f32(gpu_device):
+    check(W.make_workload(MIXED16, 32, 8, 128, 16, q_dtype=torch.float32,
+                          kv_dtype=torch.float32, seed=3, name="f32"), gpu_device)
+
+
+def test_non_causal(gpu_device):
+    check(W.make_workload([(5, 40), (16, 16), (1, 70)], 8, 2, 128, 16, seed=8, name="nc"),
+          gpu_device, use_causal_mask=False)
+
+
+@pytest.mark.parametrize("kv_len,q_len", [(48, 16), (33, 1)])
+def test_skip_kv_update(gpu_device, kv_len, q_len):
+    w = W.make_workload([(q_len, kv_len)], 4, 2, 128, 16, seed=9, name="skip")
+    exp_out, _ = O.ref_ragged_paged_attention(*w.args(), mode="fp32", skip_kv_update=True,
+                                              **w.kwargs)
+    out, cache = run_gpu(w, gpu_device, skip_kv_update=True)
+    assert_close(out, exp_out, 2e-2, 2e-2, "skip_kv_update output")
+    assert bytes_equal(cache, w.kv_cache)
+
+
+def test_nan_poison_isolation(gpu_device):
+    w = W.make_workload([(1, k) for k in (129, 2048, 8, 7, 257, 259, 8, 511)], 8, 2, 128, 16,
+                        seed=10, nan_fill=True, max_num_seqs=10, max_num_tokens=12,
+                        name="nan-decode")
+    out = check(w, gpu_device)
+    assert torch.isfinite(out).all()
+    w = W.make_workload([(q, q + 40) for q in (5, 33, 1, 64)], 8, 2, 128, 16, seed=11,
+                        nan_fill=True, name="nan-prefill")
+    out = check(w, gpu_device)
+    assert torch.isfinite(out).all()
+
+
+def test_nan_sequence_stays_in_its_rows(gpu_device):
+    w = W.make_workload([(3, 40), (1, 100), (5, 77)], 8, 2, 128, 16, seed=12, name="nanseq")
+    S = w.kv_lens.shape[0]
+    pps = w.page_indices.shape[0] // S
+    pages = w.page_indices[pps:pps + O.cdiv(100, 16)].long()
+    w.kv_cache[pages] = float("nan")
+    out, _ = run_gpu(w, gpu_device)
+    assert torch.isnan(out[3:4].float()).all()
+    assert torch.isfinite(out[:3].float()).all() and torch.isfinite(out[4:].float()).all()
+
+
+def test_bundled_matches_flat(gpu_device):
+    """test_rpa_bundled.py:173-227: bundled block-major == per-layer flat, bitwise."""
+    layers, P = 3, 96
+    w = W.make_workload([(1, 128)] * 4 + [(32, 192)] * 4, 16, 4, 128, 16, seed=13,
+                        num_pages=P, distribution=[4, 8, 8], name="bundled")
+    g = torch.Generator().manual_seed(0)
+    init = torch.randn(layers, *w.kv_cache.shape, generator=g).to(BF16)
+    dev = gpu_device
+    for layer in range(layers):
+        flat = w.to(dev)
+        flat_cache = init[layer].clone().to(dev)
+        out_ref, _ = R.ragged_paged_attention(flat.q, flat.k, flat.v, flat_cache, flat.kv_lens,
+                                              flat.page_indices, flat.cu_q_lens,
+                                              flat.distribution, **w.kwargs)
+        bundle = init.clone().transpose(0, 1).contiguous().to(dev)
+        out_b, bundle = R.ragged_paged_attention_bundled(
+            flat.q, flat.k, flat.v, bundle, layer, flat.kv_lens, flat.page_indices,
+            flat.cu_q_lens, flat.distribution, **w.kwargs)
+        torch.cuda.synchronize()
+        n = w.num_tokens
+        assert bytes_equal(out_ref[:n].cpu(), out_b[:n].cpu())
+        assert bytes_equal(flat_cache.cpu(), bundle[:, layer].cpu())
+        others = [x for x in range(layers) if x != layer]
+        assert bytes_equal(bundle[:, others].cpu(), init.transpose(0, 1)[:, others].contiguous())
+
+
+# ---------------------------------------------------------------------------
+# BASELINE configurations at full size
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("idx", [1, 2, 3, 4, 5])
+def test_baseline_config(gpu_device, idx):
+    check(W.baseline_config(idx), gpu_device)

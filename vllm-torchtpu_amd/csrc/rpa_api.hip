@@ -1,0 +1,154 @@
+// C ABI of librpa_hip.so (declared in include/rpa.h).
+//
+// Host-side only: validates the descriptor, derives the launch parameters and
+// enqueues the kernels on the caller's stream.  No allocation, no host sync.
+#include <math.h>
+#include <string.h>
+
+#include "rpa.h"
+#include "rpa_common.h"
+#include "rpa_internal.h"
+
+namespace {
+
+int dtype_bytes(int dt) {
+  switch (dt) {
+    case RPA_DTYPE_F32: return 4;
+    case RPA_DTYPE_BF16:
+    case RPA_DTYPE_F16: return 2;
+    case RPA_DTYPE_FP8_E4M3FN:
+    case RPA_DTYPE_FP8_E5M2: return 1;
+    default: return 0;
+  }
+}
+
+int64_t cdiv64(int64_t a, int64_t b) { return (a + b - 1) / b; }
+int64_t align64(int64_t x, int64_t a) { return cdiv64(x, a) * a; }
+
+rpa::Params make_params(const rpa_desc* d) {
+  rpa::Params p;
+  memset(&p, 0, sizeof(p));
+  p.T = d->max_num_tokens;
+  p.Hq = d->num_q_heads;
+  p.Hkv = d->num_kv_heads;
+  p.qpk = d->num_q_heads / d->num_kv_heads;
+  p.D = d->head_dim;
+  p.Dp = d->head_dim_padded;
+  p.P = d->total_num_pages;
+  p.ps = d->page_size;
+  p.Kx2 = d->kv_heads_x2;
+  p.S = d->max_num_seqs;
+  p.pps = d->pages_per_seq;
+  p.causal = d->use_causal_mask ? 1 : 0;
+  p.window = d->sliding_window > 0 ? d->sliding_window : 0;
+  p.has_cap = d->has_soft_cap ? 1 : 0;
+  p.cap = d->soft_cap;
+  p.inv_cap = d->has_soft_cap ? 1.0f / d->soft_cap : 0.0f;
+  p.score_scale = d->sm_scale * d->k_scale * d->q_scale;
+  p.v_scale = d->v_scale;
+  p.rec = static_cast<int64_t>(d->kv_heads_x2) * d->head_dim_padded;
+  return p;
+}
+
+}  // namespace
+
+extern "C" {
+
+int rpa_abi_version(void) { return RPA_ABI_VERSION; }
+
+const char* rpa_status_str(int status) {
+  switch (status) {
+    case RPA_OK: return "ok";
+    case RPA_ERR_INVALID_ARG: return "invalid argument: descriptor violates the RPA input contract";
+    case RPA_ERR_UNSUPPORTED: return "unsupported: valid RPA input not implemented by this library";
+    case RPA_ERR_WORKSPACE: return "workspace missing or smaller than rpa_workspace_size()";
+    case RPA_ERR_LAUNCH: return "HIP kernel launch failed";
+    case RPA_ERR_NULL_PTR: return "a required device pointer is NULL";
+    case RPA_ERR_ABI: return "rpa_desc.abi_version does not match the library";
+    default: return "unknown status";
+  }
+}
+
+int rpa_get_kv_cache_shape(int32_t total_num_pages, int32_t page_size, int32_t num_kv_heads,
+                           int32_t head_dim, int32_t kv_dtype, int64_t shape_out[5]) {
+  const int b = dtype_bytes(kv_dtype);
+  if (b == 0 || shape_out == nullptr) return RPA_ERR_INVALID_ARG;
+  const int pack = 4 / b;
+  shape_out[0] = total_num_pages;
+  shape_out[1] = page_size;
+  shape_out[2] = align64(2LL * num_kv_heads, pack) / pack;
+  shape_out[3] = pack;
+  shape_out[4] = align64(head_dim, 128);
+  return RPA_OK;
+}
+
+int rpa_validate_desc(const rpa_desc* d) {
+  if (d == nullptr) return RPA_ERR_NULL_PTR;
+  if (d->abi_version != RPA_ABI_VERSION) return RPA_ERR_ABI;
+  const int kvb = dtype_bytes(d->kv_dtype);
+  if (kvb == 0 || dtype_bytes(d->q_dtype) == 0) return RPA_ERR_INVALID_ARG;
+  if (d->num_q_heads <= 0 || d->num_kv_heads <= 0 || d->head_dim <= 0) return RPA_ERR_INVALID_ARG;
+  if (d->num_q_heads % d->num_kv_heads != 0) return RPA_ERR_INVALID_ARG;
+  const int pack = 4 / kvb;
+  if (d->kv_packing != pack) return RPA_ERR_INVALID_ARG;
+  if (d->head_dim_padded != align64(d->head_dim, 128)) return RPA_ERR_INVALID_ARG;
+  if (d->kv_heads_x2 != align64(2LL * d->num_kv_heads, pack)) return RPA_ERR_INVALID_ARG;
+  if (d->page_size <= 0 || d->page_size % pack != 0) return RPA_ERR_INVALID_ARG;
+  if (d->total_num_pages <= 0 || d->max_num_tokens < 0) return RPA_ERR_INVALID_ARG;
+  if (d->max_num_seqs <= 0 || d->pages_per_seq < 0) return RPA_ERR_INVALID_ARG;
+  if (d->has_soft_cap && d->soft_cap == 0.0f) return RPA_ERR_INVALID_ARG;
+  if (d->sliding_window < 0) return RPA_ERR_INVALID_ARG;
+  // Implemented combinations.
+  if (d->kv_dtype == RPA_DTYPE_F16 || d->q_dtype == RPA_DTYPE_F16) return RPA_ERR_UNSUPPORTED;
+  if (d->out_dtype != RPA_DTYPE_F32 && d->out_dtype != RPA_DTYPE_BF16) return RPA_ERR_UNSUPPORTED;
+  const bool q_is_fp8 = d->q_dtype == RPA_DTYPE_FP8_E4M3FN || d->q_dtype == RPA_DTYPE_FP8_E5M2;
+  if (q_is_fp8 && d->q_dtype != d->kv_dtype) return RPA_ERR_UNSUPPORTED;
+  if (d->head_dim_padded > 512) return RPA_ERR_UNSUPPORTED;
+  return RPA_OK;
+}
+
+size_t rpa_workspace_size(const rpa_desc* d) {
+  if (rpa_validate_desc(d) != RPA_OK) return 0;
+  return 256;  // reserved; the current kernels keep all state on chip
+}
+
+int rpa_kv_cache_update(const rpa_desc* d, const void* keys, const void* values, void* kv_cache,
+                        const int32_t* kv_lens, const int32_t* page_indices,
+                        const int32_t* cu_q_lens, const int32_t* distribution, void* stream) {
+  const int st = rpa_validate_desc(d);
+  if (st != RPA_OK) return st;
+  if (d->max_num_tokens == 0) return RPA_OK;
+  if (!keys || !values || !kv_cache || !kv_lens || !page_indices || !cu_q_lens || !distribution)
+    return RPA_ERR_NULL_PTR;
+  const rpa::Params p = make_params(d);
+  hipError_t e = rpa::launch_kv_update(p, dtype_bytes(d->kv_dtype), keys, values, kv_cache,
+                                       kv_lens, page_indices, cu_q_lens, distribution,
+                                       static_cast<hipStream_t>(stream));
+  return e == hipSuccess ? RPA_OK : RPA_ERR_LAUNCH;
+}
+
+int rpa_forward(const rpa_desc* d, const void* queries, const void* keys, const void* values,
+                void* kv_cache, const int32_t* kv_lens, const int32_t* page_indices,
+                const int32_t* cu_q_lens, const int32_t* distribution, void* out,
+                void* workspace, size_t workspace_bytes, void* stream) {
+  const int st = rpa_validate_desc(d);
+  if (st != RPA_OK) return st;
+  if (d->max_num_tokens == 0) return RPA_OK;
+  if (!queries || !kv_cache || !kv_lens || !page_indices || !cu_q_lens || !distribution || !out)
+    return RPA_ERR_NULL_PTR;
+  if (workspace_bytes < rpa_workspace_size(d) || workspace == nullptr) return RPA_ERR_WORKSPACE;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const rpa::Params p = make_params(d);
+  if (!d->skip_kv_update) {
+    if (!keys || !values) return RPA_ERR_NULL_PTR;
+    hipError_t e = rpa::launch_kv_update(p, dtype_bytes(d->kv_dtype), keys, values, kv_cache,
+                                         kv_lens, page_indices, cu_q_lens, distribution, s);
+    if (e != hipSuccess) return RPA_ERR_LAUNCH;
+  }
+  hipError_t e = rpa::launch_attn_generic(p, d->q_dtype, d->kv_dtype, d->out_dtype, queries,
+                                          kv_cache, kv_lens, page_indices, cu_q_lens,
+                                          distribution, out, s);
+  return e == hipSuccess ? RPA_OK : RPA_ERR_LAUNCH;
+}
+
+}  // extern "C"

@@ -1,0 +1,155 @@
+// Shared device-side definitions for the gfx950 RPA kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "rpa.h"
+
+namespace rpa {
+
+// ---------------------------------------------------------------------------
+// Launch parameters.  Built once on the host from rpa_desc; passed by value.
+// Element strides are in elements of the tensor's own dtype.
+// ---------------------------------------------------------------------------
+struct Params {
+  int32_t T;       // max_num_tokens
+  int32_t Hq;      // num_q_heads
+  int32_t Hkv;     // num_kv_heads
+  int32_t qpk;     // Hq / Hkv
+  int32_t D;       // actual head_dim
+  int32_t Dp;      // padded head_dim (cache last axis)
+  int32_t P;       // total_num_pages
+  int32_t ps;      // page_size
+  int32_t Kx2;     // combined heads per record (padded)
+  int32_t S;       // max_num_seqs
+  int32_t pps;     // pages_per_seq
+  int32_t causal;  // use_causal_mask
+  int32_t window;  // sliding_window, <= 0 = none
+  int32_t has_cap;
+  float cap;
+  float inv_cap;
+  float score_scale;  // sm_scale * k_scale * q_scale
+  float v_scale;
+  int64_t rec;  // elements per token record = Kx2 * Dp
+};
+
+// ---------------------------------------------------------------------------
+// Scalar conversions, written from the format definitions.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float bf16_bits_to_f32(uint16_t b) {
+  return __uint_as_float(static_cast<uint32_t>(b) << 16);
+}
+
+// Round-to-nearest-even f32 -> bf16 bits; NaN stays a quiet NaN.
+__device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<uint16_t>((u >> 16) | 0x40u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return static_cast<uint16_t>(u >> 16);
+}
+
+// OCP fp8 e4m3fn: 1 sign, 4 exponent (bias 7), 3 mantissa; S.1111.111 = NaN,
+// no infinities; subnormals are m * 2^-9.
+__device__ __forceinline__ float fp8e4m3_to_f32(uint8_t x) {
+  const uint32_t e = (x >> 3) & 0xfu;
+  const uint32_t m = x & 7u;
+  float v;
+  if (e == 0xfu && m == 7u) {
+    v = __uint_as_float(0x7fc00000u);
+  } else if (e == 0u) {
+    v = static_cast<float>(m) * 0x1p-9f;
+  } else {
+    v = __uint_as_float(((e + 120u) << 23) | (m << 20));
+  }
+  return (x & 0x80u) ? -v : v;
+}
+
+// OCP fp8 e5m2 is the upper byte of an IEEE binary16.
+__device__ __forceinline__ float fp8e5m2_to_f32(uint8_t x) {
+  const uint16_t h = static_cast<uint16_t>(x) << 8;
+  return static_cast<float>(__builtin_bit_cast(_Float16, h));
+}
+
+__device__ __forceinline__ float f16_bits_to_f32(uint16_t h) {
+  return static_cast<float>(__builtin_bit_cast(_Float16, h));
+}
+
+// Element-type tags: storage type + conversion to f32.
+struct TF32 {
+  using storage = float;
+  static __device__ __forceinline__ float load(const storage* p, int64_t i) { return p[i]; }
+};
+struct TBF16 {
+  using storage = uint16_t;
+  static __device__ __forceinline__ float load(const storage* p, int64_t i) {
+    return bf16_bits_to_f32(p[i]);
+  }
+};
+struct TF16 {
+  using storage = uint16_t;
+  static __device__ __forceinline__ float load(const storage* p, int64_t i) {
+    return f16_bits_to_f32(p[i]);
+  }
+};
+struct TE4M3 {
+  using storage = uint8_t;
+  static __device__ __forceinline__ float load(const storage* p, int64_t i) {
+    return fp8e4m3_to_f32(p[i]);
+  }
+};
+struct TE5M2 {
+  using storage = uint8_t;
+  static __device__ __forceinline__ float load(const storage* p, int64_t i) {
+    return fp8e5m2_to_f32(p[i]);
+  }
+};
+
+// Output stores.
+__device__ __forceinline__ void store_out(float* p, int64_t i, float v) { p[i] = v; }
+__device__ __forceinline__ void store_out(uint16_t* p, int64_t i, float v) {
+  p[i] = f32_to_bf16_bits(v);
+}
+
+// ---------------------------------------------------------------------------
+// Metadata helpers (all reads are clamped so bad metadata cannot address
+// memory outside the tensors).
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ int32_t num_seqs_of(const int32_t* distribution, int32_t S) {
+  int32_t n = distribution[2];
+  return n < 0 ? 0 : (n > S ? S : n);
+}
+
+// Largest s in [0, n) with cu[s] <= t (cu non-decreasing); -1 if none.
+__device__ __forceinline__ int32_t find_seq(const int32_t* cu, int32_t n, int32_t t) {
+  int32_t lo = 0, hi = n;  // answer in [lo, hi)
+  if (n <= 0 || cu[0] > t) return -1;
+  while (hi - lo > 1) {
+    int32_t mid = (lo + hi) >> 1;
+    if (cu[mid] <= t) lo = mid; else hi = mid;
+  }
+  return lo;
+}
+
+__device__ __forceinline__ float warp_max(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+__device__ __forceinline__ float warp_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+// logit transform shared by every attention kernel: scale then soft cap
+// (kernel.py:185-194): s = cap * tanh(s / cap).  tanh is built from exp:
+// tanh(x) = 1 - 2 / (exp(2x) + 1), exact at the limits (+-1) and odd.
+__device__ __forceinline__ float soft_cap_fn(float s, float cap, float inv_cap) {
+  const float x = s * inv_cap;
+  const float e = __expf(2.0f * x);
+  const float t = 1.0f - 2.0f / (e + 1.0f);
+  return cap * t;
+}
+
+}  // namespace rpa

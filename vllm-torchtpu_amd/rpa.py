@@ -1,0 +1,432 @@
+"""Ragged Paged Attention on MI355X: host-side mirror of the reference API.
+
+Mirrors `vllm_torchtpu.kernels.ragged_paged_attention.v3.kernel`
+(reference file src/vllm_torchtpu/kernels/ragged_paged_attention/v3/kernel.py,
+"kernel.py" below): same function names, positional order, keyword names and
+defaults, same `ValueError` conditions.  The compute is the HIP library
+`librpa_hip.so` (C ABI in include/rpa.h); this module only validates,
+describes the call and passes device pointers plus the current HIP stream.
+
+Deliberate differences from the Pallas entry point, each also recorded in
+the design notes:
+  * The cache is updated in place (the reference donates and aliases it,
+    kernel.py:1631, :1908); the returned cache is the same tensor.
+  * The output is a fresh [T, Hq, D] tensor in the q dtype (the reference
+    aliases it to the donated q buffer, so rows past cu_q_lens[num_seqs] hold
+    stale data there and undefined data here).
+  * All sequences [0, distribution[2]) are computed, as in
+    ref_ragged_paged_attention (kernel.py:143); the Pallas call skips the
+    [distribution[0], distribution[1]) segment unless chunk_prefill_size is
+    given (kernel.py:1958-1966).  The runner emits distribution[0] ==
+    distribution[1], where both agree.
+  * Accumulation is fp32 whatever out_dtype says (out_dtype selects the
+    Pallas accumulator precision, kernel.py:1820-1829).
+  * Tiling knobs (*_block_sizes, vmem_limit_bytes, chunk_prefill_size) are
+    validated like the reference and otherwise ignored; debug_mode and the
+    disable_* checks have no effect.
+"""
+
+from __future__ import annotations
+
+import enum
+from typing import Any
+
+import torch
+
+from . import _native as N
+from .util import align_to, cdiv, get_dtype_packing
+
+__all__ = [
+    "RpaCase",
+    "get_kv_cache_shape",
+    "merge_kv",
+    "static_validate_inputs",
+    "dynamic_validate_inputs",
+    "ragged_paged_attention",
+    "ragged_paged_attention_bundled",
+    "rpa_kv_cache_update",
+]
+
+
+class RpaCase(enum.Enum):
+    """Segments of `distribution` (kernel.py:42-71)."""
+
+    DECODE = 0
+    PREFILL = 1
+    MIXED = 2
+
+    @property
+    def symbol(self) -> str:
+        return {RpaCase.DECODE: "d", RpaCase.PREFILL: "p", RpaCase.MIXED: "m"}[self]
+
+    def get_range(self, distribution):
+        assert tuple(distribution.shape) == (3,)
+        if self == RpaCase.DECODE:
+            return 0, distribution[0]
+        if self == RpaCase.PREFILL:
+            return distribution[0], distribution[1]
+        return distribution[1], distribution[2]
+
+
+def get_kv_cache_shape(total_num_pages, page_size, actual_num_kv_heads,
+                       actual_head_dim, kv_dtype):
+    """Paged cache shape (kernel.py:278-292):
+    [P, page_size, align(2*Hkv, pack) // pack, pack, align(D, 128)]."""
+    kv_packing = get_dtype_packing(kv_dtype)
+    return (
+        total_num_pages,
+        page_size,
+        align_to(actual_num_kv_heads * 2, kv_packing) // kv_packing,
+        kv_packing,
+        align_to(actual_head_dim, 128),
+    )
+
+
+def merge_kv(k: torch.Tensor, v: torch.Tensor) -> torch.Tensor:
+    """Cache records for k/v rows (kernel.py:1140-1168): combined head 2h = K_h,
+    2h+1 = V_h, zero padding of heads to the packing and dims to 128."""
+    assert k.shape == v.shape and k.dtype == v.dtype
+    t, hkv, d = k.shape
+    pack = get_dtype_packing(k.dtype)
+    hx2 = align_to(2 * hkv, pack)
+    dp = align_to(d, 128)
+    out = torch.zeros((t, hx2, dp), dtype=k.dtype, device=k.device)
+    out[:, :2 * hkv, :d] = torch.cat([k, v], dim=-1).reshape(t, 2 * hkv, d)
+    return out.reshape(t, hx2 // pack, pack, dp)
+
+
+def static_validate_inputs(queries, keys, values, kv_cache, kv_lens, page_indices,
+                           cu_q_lens, distribution, *, use_causal_mask=True,
+                           skip_kv_mask=False, sm_scale=1.0, sliding_window=None,
+                           soft_cap=None, out_dtype=None, mask_value=None,
+                           q_scale=None, k_scale=None, v_scale=None,
+                           chunk_prefill_size=None, d_block_sizes=None,
+                           p_block_sizes=None, m_block_sizes=None,
+                           vmem_limit_bytes=None):
+    """Shape and dtype rules, raising ValueError (kernel.py:1366-1538)."""
+    q, k, v = queries, keys, values
+    if use_causal_mask and skip_kv_mask:
+        raise ValueError("Can not skip kv mask when using causal mask.")
+    if not (q.dim() == k.dim() == v.dim() == 3):
+        raise ValueError(f"Expected 3D array for {q.shape=}, {k.shape=}, {v.shape=}")
+    if k.shape != v.shape:
+        raise ValueError(f"Expected {k.shape=} to be equal to {v.shape=}")
+    if not (q.shape[0] == k.shape[0] == v.shape[0]):
+        raise ValueError(
+            f"Expected {q.shape[0]=} to be equal to {k.shape[0]=} and {v.shape[0]=}")
+    if not (q.shape[2] == k.shape[2] == v.shape[2]):
+        raise ValueError(
+            f"Expected {q.shape[2]=} to be equal to {k.shape[2]=} and {v.shape[2]=}")
+    actual_head_dim, actual_num_q_heads, actual_num_kv_heads = q.shape[2], q.shape[1], k.shape[1]
+    if actual_num_q_heads % actual_num_kv_heads != 0:
+        raise ValueError(
+            f"Expected {actual_num_q_heads=} to be divisible by {actual_num_kv_heads=}.")
+    expected = get_kv_cache_shape(kv_cache.shape[0], kv_cache.shape[1], actual_num_kv_heads,
+                                  actual_head_dim, kv_cache.dtype)
+    if tuple(kv_cache.shape) != tuple(expected):
+        raise ValueError(f"Expected {kv_cache.shape=} to be equal to {expected=}")
+    _, page_size, hx2_per_pack, kv_packing, head_dim = kv_cache.shape
+    if head_dim != align_to(actual_head_dim, 128):
+        raise ValueError(f"Expected {head_dim=} is equal to {align_to(actual_head_dim, 128)=}")
+    if not (kv_cache.dtype == k.dtype == v.dtype):
+        raise ValueError(
+            f"Expected {kv_cache.dtype=} to be equal to {k.dtype=} and {v.dtype=}.")
+    if not kv_cache.dtype.is_floating_point:
+        raise ValueError(f"Expected {kv_cache.dtype=} to be a floating point.")
+    if kv_packing != get_dtype_packing(kv_cache.dtype):
+        raise ValueError(f"{kv_packing=} does not match with {kv_cache.dtype=}")
+    hx2 = hx2_per_pack * kv_packing
+    if hx2 % 2 != 0:
+        raise ValueError(f"Combined KV heads must be divisible by 2, but got {hx2}")
+    if hx2 % kv_packing != 0 or hx2 // 2 < actual_num_kv_heads:
+        raise ValueError(f"Invalid {hx2=}, {actual_num_kv_heads=}, {kv_packing=}")
+    if not (torch.int32 == kv_lens.dtype == page_indices.dtype == cu_q_lens.dtype
+            == distribution.dtype):
+        raise ValueError(
+            f"Expected int32 dtype for {kv_lens.dtype=}, {page_indices.dtype=},"
+            f" {cu_q_lens.dtype=}, {distribution.dtype=}")
+    if not (kv_lens.dim() == page_indices.dim() == cu_q_lens.dim() == 1):
+        raise ValueError(
+            f"Expected 1D array for {kv_lens.shape=}, {page_indices.shape=},"
+            f" {cu_q_lens.shape=}")
+    max_num_seqs = kv_lens.shape[0]
+    num_page_indices = page_indices.shape[0]
+    if max_num_seqs == 0 or num_page_indices % max_num_seqs != 0:
+        raise ValueError(f"Expected {num_page_indices=} to be divisible by {max_num_seqs=}.")
+    if tuple(cu_q_lens.shape) != (max_num_seqs + 1,):
+        raise ValueError(f"Expected {cu_q_lens.shape=} to be ({max_num_seqs + 1},).")
+    if tuple(distribution.shape) != (3,):
+        raise ValueError(f"Expected {distribution.shape=} to be (3,).")
+    if page_size % kv_packing != 0:
+        raise ValueError(f"{page_size=} must be divisible by {kv_packing=}.")
+    if sliding_window is not None and sliding_window <= 0:
+        raise ValueError(f"{sliding_window=} must be positive.")
+    if soft_cap is not None and soft_cap == 0.0:
+        raise ValueError(f"{soft_cap=} must not be 0.0.")
+    if chunk_prefill_size is not None and chunk_prefill_size <= 0:
+        raise ValueError(f"{chunk_prefill_size=} must be positive.")
+    for block_sizes, prefix in ((d_block_sizes, "decode"), (p_block_sizes, "prefill"),
+                                (m_block_sizes, "mixed")):
+        if block_sizes is None:
+            continue
+        bq_sz, bkv_sz, bq_csz, bkv_csz = block_sizes
+        if not (bq_csz > 0 and bq_sz % bq_csz == 0):
+            raise ValueError(f"{prefix} {bq_csz=} and {bq_sz=} must satisfy "
+                             "(0 < bq_csz and bq_sz % bq_csz == 0).")
+        if not (bkv_csz > 0 and bkv_sz % bkv_csz == 0):
+            raise ValueError(f"{prefix} {bkv_csz=} and {bkv_sz=} must satisfy "
+                             "(0 < bkv_csz and bkv_sz % bkv_csz == 0).")
+        if bkv_sz % page_size != 0:
+            raise ValueError(f"{prefix} {bkv_sz=} must be divisible by {page_size=}.")
+        if bkv_csz % page_size != 0:
+            raise ValueError(f"{prefix} {bkv_csz=} must be divisible by {page_size=}.")
+    if vmem_limit_bytes is not None and vmem_limit_bytes <= 0:
+        raise ValueError(f"{vmem_limit_bytes=} must be positive.")
+
+
+def dynamic_validate_inputs(queries, keys, values, kv_cache, kv_lens, page_indices,
+                            cu_q_lens, distribution, **kwargs):
+    """Metadata value rules (kernel.py:1273-1362).  Reads the metadata back to
+    the host, so it synchronises; the reference likewise runs it only in its
+    CPU reference path (kernel.py:103-122), never inside the kernel call."""
+    static_validate_inputs(queries, keys, values, kv_cache, kv_lens, page_indices,
+                           cu_q_lens, distribution, **kwargs)
+    max_num_tokens = queries.shape[0]
+    total_num_pages, page_size = kv_cache.shape[0], kv_cache.shape[1]
+    max_num_seqs = kv_lens.shape[0]
+    pages_per_seq = page_indices.shape[0] // max_num_seqs
+    i, j, k = (int(x) for x in distribution.cpu().tolist())
+    if not (i <= j <= k):
+        raise ValueError(f"Invalid distribution: {(i, j, k)=}")
+    if k > max_num_seqs:
+        raise ValueError(f"num_seqs={k} must be <= {max_num_seqs=}")
+    cu = cu_q_lens.cpu().tolist()
+    kvl = kv_lens.cpu().tolist()
+    pi = page_indices.cpu().tolist()
+    if cu[k] > max_num_tokens:
+        raise ValueError(f"Total q tokens {cu[k]} must be <= {max_num_tokens=}.")
+    for s in range(k):
+        q_len = cu[s + 1] - cu[s]
+        kv_len = kvl[s]
+        if not (0 < q_len <= kv_len):
+            raise ValueError(f"Require 0 < {q_len=} <= {kv_len=} at sequence {s}.")
+        page_cnt = cdiv(kv_len, page_size)
+        if page_cnt > pages_per_seq:
+            raise ValueError(f"Require {page_cnt=} <= {pages_per_seq=} at sequence {s} where"
+                             f" {kv_len=} and {page_size=}.")
+        for p in range(page_cnt):
+            page_idx = pi[s * pages_per_seq + p]
+            if not (0 <= page_idx < total_num_pages):
+                raise ValueError(f"Require 0 <= {page_idx=} < {total_num_pages=} at sequence"
+                                 f" {s} where {kv_len=} and {page_size=}.")
+
+
+# ---------------------------------------------------------------------------
+# Descriptor + native call
+# ---------------------------------------------------------------------------
+def _make_desc(q, k, kv_cache, kv_lens, page_indices, out_dtype, *, use_causal_mask,
+               skip_kv_update, sm_scale, sliding_window, soft_cap, q_scale, k_scale,
+               v_scale, path=N.RPA_PATH_AUTO) -> N.RpaDesc:
+    d = N.RpaDesc()
+    d.abi_version = N.ABI_VERSION
+    d.q_dtype = N.rpa_dtype(q.dtype)
+    d.kv_dtype = N.rpa_dtype(kv_cache.dtype)
+    d.out_dtype = N.rpa_dtype(out_dtype)
+    d.max_num_tokens = q.shape[0]
+    d.num_q_heads = q.shape[1]
+    d.num_kv_heads = k.shape[1]
+    d.head_dim = q.shape[2]
+    d.head_dim_padded = kv_cache.shape[4]
+    d.total_num_pages = kv_cache.shape[0]
+    d.page_size = kv_cache.shape[1]
+    d.kv_packing = kv_cache.shape[3]
+    d.kv_heads_x2 = kv_cache.shape[2] * kv_cache.shape[3]
+    d.max_num_seqs = kv_lens.shape[0]
+    d.pages_per_seq = page_indices.shape[0] // kv_lens.shape[0]
+    d.use_causal_mask = int(bool(use_causal_mask))
+    d.skip_kv_update = int(bool(skip_kv_update))
+    d.sliding_window = 0 if sliding_window is None else int(sliding_window)
+    d.has_soft_cap = int(soft_cap is not None)
+    d.soft_cap = float(soft_cap) if soft_cap is not None else 0.0
+    d.sm_scale = float(sm_scale)
+    d.q_scale = 1.0 if q_scale is None else float(q_scale)
+    d.k_scale = 1.0 if k_scale is None else float(k_scale)
+    d.v_scale = 1.0 if v_scale is None else float(v_scale)
+    d.path = int(path)
+    return d
+
+
+def _ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def _require_device(*tensors: torch.Tensor) -> torch.device:
+    dev = tensors[0].device
+    if dev.type != "cuda":
+        raise RuntimeError(
+            "ragged_paged_attention runs on the MI355X HIP library only; got tensors on "
+            f"{dev} (there is no CPU path)")
+    for t in tensors:
+        if t.device != dev:
+            raise ValueError(f"all tensors must be on {dev}, got {t.device}")
+    return dev
+
+
+def _rpa_forward_impl(queries, keys, values, kv_cache, kv_lens, page_indices, cu_q_lens,
+                      distribution, out, *, use_causal_mask, skip_kv_update, sm_scale,
+                      sliding_window, soft_cap, q_scale, k_scale, v_scale,
+                      path=N.RPA_PATH_AUTO, workspace=None):
+    L = N.lib()
+    _require_device(queries, keys, values, kv_cache, kv_lens, page_indices, cu_q_lens,
+                    distribution, out)
+    for name, t in (("queries", queries), ("keys", keys), ("values", values),
+                    ("kv_cache", kv_cache), ("kv_lens", kv_lens),
+                    ("page_indices", page_indices), ("cu_q_lens", cu_q_lens),
+                    ("distribution", distribution), ("out", out)):
+        if not t.is_contiguous():
+            raise ValueError(f"{name} must be contiguous")
+    desc = _make_desc(queries, keys, kv_cache, kv_lens, page_indices, out.dtype,
+                      use_causal_mask=use_causal_mask, skip_kv_update=skip_kv_update,
+                      sm_scale=sm_scale, sliding_window=sliding_window, soft_cap=soft_cap,
+                      q_scale=q_scale, k_scale=k_scale, v_scale=v_scale, path=path)
+    N.check(L.rpa_validate_desc(desc), "rpa_validate_desc")
+    ws_bytes = int(L.rpa_workspace_size(desc))
+    if workspace is None or workspace.numel() < ws_bytes:
+        workspace = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=queries.device)
+    stream = torch.cuda.current_stream(queries.device).cuda_stream
+    with torch.cuda.device(queries.device):
+        code = L.rpa_forward(desc, _ptr(queries), _ptr(keys), _ptr(values), _ptr(kv_cache),
+                             _ptr(kv_lens), _ptr(page_indices), _ptr(cu_q_lens),
+                             _ptr(distribution), _ptr(out), _ptr(workspace),
+                             ws_bytes, stream)
+    N.check(code, "rpa_forward")
+    return out
+
+
+# torch custom op: opaque to torch.compile, mutates the cache in place
+# (mirrors the reference's torch-facing op, attention.py:1157-1189).
+@torch.library.custom_op("rpa_amd::ragged_paged_attention", mutates_args=("kv_cache",))
+def _rpa_op(queries: torch.Tensor, keys: torch.Tensor, values: torch.Tensor,
+            kv_cache: torch.Tensor, kv_lens: torch.Tensor, page_indices: torch.Tensor,
+            cu_q_lens: torch.Tensor, distribution: torch.Tensor, out_dtype: torch.dtype,
+            use_causal_mask: bool, skip_kv_update: bool, sm_scale: float,
+            sliding_window: int, soft_cap: float, has_soft_cap: bool, q_scale: float,
+            k_scale: float, v_scale: float, path: int) -> torch.Tensor:
+    out = torch.empty(queries.shape, dtype=out_dtype, device=queries.device)
+    return _rpa_forward_impl(
+        queries, keys, values, kv_cache, kv_lens, page_indices, cu_q_lens, distribution, out,
+        use_causal_mask=use_causal_mask, skip_kv_update=skip_kv_update, sm_scale=sm_scale,
+        sliding_window=sliding_window if sliding_window > 0 else None,
+        soft_cap=soft_cap if has_soft_cap else None, q_scale=q_scale, k_scale=k_scale,
+        v_scale=v_scale, path=path)
+
+
+@_rpa_op.register_fake
+def _(queries, keys, values, kv_cache, kv_lens, page_indices, cu_q_lens, distribution,
+      out_dtype, use_causal_mask, skip_kv_update, sm_scale, sliding_window, soft_cap,
+      has_soft_cap, q_scale, k_scale, v_scale, path):
+    return torch.empty(queries.shape, dtype=out_dtype, device=queries.device)
+
+
+def ragged_paged_attention(
+    queries: torch.Tensor,  # [max_num_tokens, actual_num_q_heads, actual_head_dim]
+    keys: torch.Tensor,  # [max_num_tokens, actual_num_kv_heads, actual_head_dim]
+    values: torch.Tensor,  # [max_num_tokens, actual_num_kv_heads, actual_head_dim]
+    # [total_num_pages, page_size, num_kv_heads_x2 // kv_packing, kv_packing, head_dim]
+    kv_cache: torch.Tensor,
+    kv_lens: torch.Tensor,  # i32[max_num_seqs]
+    page_indices: torch.Tensor,  # i32[max_num_seqs * pages_per_seq]
+    cu_q_lens: torch.Tensor,  # i32[max_num_seqs + 1]
+    distribution: torch.Tensor,  # i32[3]
+    *,
+    use_causal_mask: bool = True,
+    skip_kv_mask: bool = False,
+    skip_kv_update: bool = False,
+    sm_scale: float = 1.0,
+    sliding_window: int | None = None,
+    soft_cap: float | None = None,
+    out_dtype: Any = None,
+    mask_value: float | None = None,
+    q_scale: float | None = None,
+    k_scale: float | None = None,
+    v_scale: float | None = None,
+    chunk_prefill_size: int | None = None,
+    d_block_sizes: tuple[int, int, int, int] | None = None,
+    p_block_sizes: tuple[int, int, int, int] | None = None,
+    m_block_sizes: tuple[int, int, int, int] | None = None,
+    vmem_limit_bytes: int | None = None,
+    debug_mode: bool = False,
+    disable_bounds_checks: bool = True,
+    disable_semaphore_checks: bool = True,
+):
+    """Ragged paged attention with mixed prefill and decode (kernel.py:1633-1984).
+
+    Returns (out [max_num_tokens, Hq, D] in the q dtype, kv_cache).  kv_cache is
+    updated in place with the new tokens' K/V (unless skip_kv_update) and
+    returned.  Rows of `out` at or beyond cu_q_lens[distribution[2]] are not
+    written.  See the module docstring for the deliberate differences.
+    """
+    del debug_mode, disable_bounds_checks, disable_semaphore_checks
+    static_validate_inputs(
+        queries, keys, values, kv_cache, kv_lens, page_indices, cu_q_lens, distribution,
+        use_causal_mask=use_causal_mask, skip_kv_mask=skip_kv_mask, sm_scale=sm_scale,
+        sliding_window=sliding_window, soft_cap=soft_cap, out_dtype=out_dtype,
+        mask_value=mask_value, q_scale=q_scale, k_scale=k_scale, v_scale=v_scale,
+        chunk_prefill_size=chunk_prefill_size, d_block_sizes=d_block_sizes,
+        p_block_sizes=p_block_sizes, m_block_sizes=m_block_sizes,
+        vmem_limit_bytes=vmem_limit_bytes)
+    if mask_value is not None and mask_value > -1e30:
+        # Masked logits are excluded with weight exactly 0; that equals the
+        # reference only when exp(mask_value - rowmax) underflows.
+        raise NotImplementedError(
+            f"{mask_value=}: only mask values <= -1e30 (default finfo.min) are supported")
+    result_dtype = queries.dtype
+    q = queries
+    if q_scale is not None:
+        # kernel.py:176-183: q / q_scale in q's dtype, clip to the KV dtype range,
+        # cast to the KV dtype; q_scale is multiplied back into the logits.
+        info = torch.finfo(kv_cache.dtype)
+        q = torch.clamp(q / q_scale, min=info.min, max=info.max).to(kv_cache.dtype)
+    out = torch.ops.rpa_amd.ragged_paged_attention(
+        q.contiguous(), keys.contiguous(), values.contiguous(), kv_cache, kv_lens, page_indices,
+        cu_q_lens, distribution, result_dtype, bool(use_causal_mask), bool(skip_kv_update),
+        float(sm_scale), 0 if sliding_window is None else int(sliding_window),
+        0.0 if soft_cap is None else float(soft_cap), soft_cap is not None,
+        1.0 if q_scale is None else float(q_scale), 1.0 if k_scale is None else float(k_scale),
+        1.0 if v_scale is None else float(v_scale), N.RPA_PATH_AUTO)
+    return out, kv_cache
+
+
+def ragged_paged_attention_bundled(queries, keys, values, kv_cache_bundle, layer_idx,
+                                   kv_lens, page_indices, cu_q_lens, distribution, **kwargs):
+    """RPA on a block-major multi-layer cache (kernel.py:2011-2061).
+
+    kv_cache_bundle is [num_pages, num_layers, page_size, ...]; it is viewed as
+    [num_pages * num_layers, page_size, ...] (no copy) and logical page p of
+    layer l maps to flat page p * num_layers + l.  Updated in place.
+    """
+    num_blocks, num_layers = kv_cache_bundle.shape[0], kv_cache_bundle.shape[1]
+    flat = kv_cache_bundle.view(num_blocks * num_layers, *kv_cache_bundle.shape[2:])
+    flat_page_indices = (page_indices * num_layers + layer_idx).to(torch.int32)
+    out, _ = ragged_paged_attention(queries, keys, values, flat, kv_lens, flat_page_indices,
+                                    cu_q_lens, distribution, **kwargs)
+    return out, kv_cache_bundle
+
+
+def rpa_kv_cache_update(keys, values, kv_cache, kv_lens, page_indices, cu_q_lens,
+                        distribution):
+    """Only the cache write of an RPA call (kernel.py:652-715), in place."""
+    L = N.lib()
+    _require_device(keys, values, kv_cache, kv_lens, page_indices, cu_q_lens, distribution)
+    desc = _make_desc(keys, keys, kv_cache, kv_lens, page_indices, torch.bfloat16,
+                      use_causal_mask=True, skip_kv_update=False, sm_scale=1.0,
+                      sliding_window=None, soft_cap=None, q_scale=None, k_scale=None,
+                      v_scale=None)
+    desc.q_dtype = desc.kv_dtype
+    stream = torch.cuda.current_stream(keys.device).cuda_stream
+    with torch.cuda.device(keys.device):
+        code = L.rpa_kv_cache_update(desc, _ptr(keys), _ptr(values), _ptr(kv_cache),
+                                     _ptr(kv_lens), _ptr(page_indices), _ptr(cu_q_lens),
+                                     _ptr(distribution), stream)
+    N.check(code, "rpa_kv_cache_update")
+    return kv_cache
