@@ -250,3 +250,58 @@ def test_bundled_matches_flat(gpu_device):
 @pytest.mark.parametrize("idx", [1, 2, 3, 4, 5])
 def test_baseline_config(gpu_device, idx):
     check(W.baseline_config(idx), gpu_device)
+
+
+# ---------------------------------------------------------------------------
+# decode path edge cases (single-token rows, split-K)
+# ---------------------------------------------------------------------------
+DECODE_EDGE = [(1, k) for k in (1, 2, 31, 32, 33, 100, 511, 512, 513, 1000, 4097, 10000)]
+
+
+@pytest.mark.parametrize("heads", [(32, 8), (16, 1), (8, 8), (12, 4)])
+@pytest.mark.parametrize("dt", [BF16, E4M3, E5M2])
+def test_decode_edges(gpu_device, heads, dt):
+    scales = dict(k_scale=0.8, v_scale=1.3) if dt != BF16 else {}
+    check(W.make_workload(DECODE_EDGE, heads[0], heads[1], 128, 16, kv_dtype=dt, seed=31,
+                          distribution=[12, 12, 12], name="decode-edge", **scales), gpu_device)
+
+
+@pytest.mark.parametrize("window,cap", [(5, None), (128, None), (1, None), (None, 30.0),
+                                        (4096, 50.0)])
+def test_decode_window_cap(gpu_device, window, cap):
+    check(W.make_workload(DECODE_EDGE, 16, 4, 128, 32, seed=32, sliding_window=window,
+                          soft_cap=cap, name="decode-wc"), gpu_device)
+
+
+@pytest.mark.parametrize("d", [256, 192, 64])
+def test_decode_head_dims(gpu_device, d):
+    check(W.make_workload(DECODE_EDGE, 16, 8, d, 16, seed=33, name=f"decode-d{d}"), gpu_device)
+
+
+def test_decode_many_seqs(gpu_device):
+    g = torch.Generator().manual_seed(34)
+    kvl = torch.randint(1, 3000, (300,), generator=g).tolist()
+    check(W.make_workload([(1, k) for k in kvl], 32, 8, 128, 16, seed=34, name="decode-300"),
+          gpu_device)
+
+
+def test_decode_f32_out(gpu_device):
+    """bf16 q with an f32 cache is not the decode path's; f32 q/out is generic."""
+    check(W.make_workload(DECODE_EDGE, 8, 2, 128, 16, q_dtype=torch.float32,
+                          kv_dtype=torch.float32, seed=35, name="decode-f32"), gpu_device)
+
+
+def test_decode_repeated_calls_reset_counters(gpu_device):
+    """The split-merge arrival counters live in a persistent workspace; every call
+    must leave them at zero, so back-to-back calls stay correct."""
+    w = W.make_workload([(1, k) for k in (4000, 33, 2048, 700, 1)], 32, 8, 128, 16, seed=36,
+                        name="decode-repeat")
+    exp_out, exp_cache = O.ref_ragged_paged_attention(*w.args(), mode="fp32", **w.kwargs)
+    g = w.to(gpu_device)
+    for rep in range(3):
+        out, cache = R.ragged_paged_attention(*g.args(), **w.kwargs)
+        torch.cuda.synchronize()
+        assert_close(out[:w.num_tokens].cpu(), exp_out, 2e-2, 2e-2, f"repeat {rep}")
+        assert bytes_equal(cache.cpu(), exp_cache)
+    # A different batch on the same workspace afterwards.
+    check(W.make_workload(DECODE_EDGE, 32, 8, 128, 16, seed=37, name="decode-after"), gpu_device)

@@ -50,6 +50,25 @@ rpa::Params make_params(const rpa_desc* d) {
   return p;
 }
 
+bool use_decode_path(const rpa_desc* d, const rpa::Params& p) {
+  return d->path != RPA_PATH_GENERIC &&
+         rpa::decode_supported(p, d->q_dtype, d->kv_dtype, d->out_dtype);
+}
+
+// Compute units of the current device (cached per device id).
+int current_num_cus() {
+  static int cache[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cache[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+      n = 256;
+    cache[dev] = n;
+  }
+  return cache[dev];
+}
+
 }  // namespace
 
 extern "C" {
@@ -109,7 +128,10 @@ int rpa_validate_desc(const rpa_desc* d) {
 
 size_t rpa_workspace_size(const rpa_desc* d) {
   if (rpa_validate_desc(d) != RPA_OK) return 0;
-  return 256;  // reserved; the current kernels keep all state on chip
+  const rpa::Params p = make_params(d);
+  size_t bytes = 256;
+  if (use_decode_path(d, p)) bytes += rpa::decode_workspace_bytes(p, dtype_bytes(d->kv_dtype));
+  return bytes;
 }
 
 int rpa_kv_cache_update(const rpa_desc* d, const void* keys, const void* values, void* kv_cache,
@@ -145,7 +167,16 @@ int rpa_forward(const rpa_desc* d, const void* queries, const void* keys, const 
                                          kv_lens, page_indices, cu_q_lens, distribution, s);
     if (e != hipSuccess) return RPA_ERR_LAUNCH;
   }
-  hipError_t e = rpa::launch_attn_generic(p, d->q_dtype, d->kv_dtype, d->out_dtype, queries,
+  rpa::Params pg = p;
+  if (use_decode_path(d, p)) {
+    const rpa::DecodeWorkspace ws = rpa::carve_decode_workspace(p, workspace, dtype_bytes(d->kv_dtype));
+    hipError_t e = rpa::launch_decode(p, d->q_dtype, d->kv_dtype, d->out_dtype, ws, queries,
+                                      kv_cache, kv_lens, page_indices, cu_q_lens, distribution,
+                                      out, current_num_cus(), s);
+    if (e != hipSuccess) return RPA_ERR_LAUNCH;
+    pg.skip_decode_rows = 1;
+  }
+  hipError_t e = rpa::launch_attn_generic(pg, d->q_dtype, d->kv_dtype, d->out_dtype, queries,
                                           kv_cache, kv_lens, page_indices, cu_q_lens,
                                           distribution, out, s);
   return e == hipSuccess ? RPA_OK : RPA_ERR_LAUNCH;

@@ -32,6 +32,7 @@ struct Params {
   float score_scale;  // sm_scale * k_scale * q_scale
   float v_scale;
   int64_t rec;  // elements per token record = Kx2 * Dp
+  int32_t skip_decode_rows;  // generic path: leave single-token rows to the decode path
 };
 
 // ---------------------------------------------------------------------------

@@ -64,6 +64,8 @@ attn_generic_kernel(Params p, const typename QT::storage* __restrict__ q,
   const int32_t q_start = cu[s];
   const int32_t q_len = cu[s + 1] - q_start;
   const int32_t kv_len = min(kv_lens[s], p.pps * p.ps);
+  // Rows the decode path owns (same predicate as its work plan).
+  if (p.skip_decode_rows && q_len == 1 && kv_len >= 1 && q_start >= 0 && q_start < p.T) return;
   const int32_t pos = kv_len - q_len + (t - q_start);
   int32_t hi = kv_len, lo = 0;
   if (p.causal) {
@@ -117,7 +119,7 @@ attn_generic_kernel(Params p, const typename QT::storage* __restrict__ q,
     }
   }
 
-  const float inv_l = l_run > 0.0f ? p.v_scale / l_run : 0.0f;
+  const float inv_l = (l_run == 0.0f) ? 0.0f : p.v_scale / l_run;
   OutS* orow = out + (static_cast<int64_t>(t) * p.Hq + g) * p.D;
 #pragma unroll
   for (int c = 0; c < kMaxChunks; ++c) {

@@ -272,6 +272,21 @@ def _require_device(*tensors: torch.Tensor) -> torch.device:
     return dev
 
 
+# Per-device workspace, zero-initialised once.  The decode path keeps arrival
+# counters in it that every call leaves at zero again, so calls that share a
+# device's workspace must be ordered on one stream (as vLLM's are).
+_WORKSPACES: dict = {}
+
+
+def _workspace(device: torch.device, nbytes: int) -> torch.Tensor:
+    key = device.index if device.index is not None else torch.cuda.current_device()
+    buf = _WORKSPACES.get(key)
+    if buf is None or buf.numel() < nbytes:
+        buf = torch.zeros(max(nbytes, 1), dtype=torch.uint8, device=device)
+        _WORKSPACES[key] = buf
+    return buf
+
+
 def _rpa_forward_impl(queries, keys, values, kv_cache, kv_lens, page_indices, cu_q_lens,
                       distribution, out, *, use_causal_mask, skip_kv_update, sm_scale,
                       sliding_window, soft_cap, q_scale, k_scale, v_scale,
@@ -290,11 +305,13 @@ def _rpa_forward_impl(queries, keys, values, kv_cache, kv_lens, page_indices, cu
                       sm_scale=sm_scale, sliding_window=sliding_window, soft_cap=soft_cap,
                       q_scale=q_scale, k_scale=k_scale, v_scale=v_scale, path=path)
     N.check(L.rpa_validate_desc(desc), "rpa_validate_desc")
-    ws_bytes = int(L.rpa_workspace_size(desc))
-    if workspace is None or workspace.numel() < ws_bytes:
-        workspace = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=queries.device)
-    stream = torch.cuda.current_stream(queries.device).cuda_stream
     with torch.cuda.device(queries.device):
+        ws_bytes = int(L.rpa_workspace_size(desc))
+        if workspace is None:
+            workspace = _workspace(queries.device, ws_bytes)
+        elif workspace.numel() < ws_bytes:
+            raise ValueError(f"workspace has {workspace.numel()} bytes, needs {ws_bytes}")
+        stream = torch.cuda.current_stream(queries.device).cuda_stream
         code = L.rpa_forward(desc, _ptr(queries), _ptr(keys), _ptr(values), _ptr(kv_cache),
                              _ptr(kv_lens), _ptr(page_indices), _ptr(cu_q_lens),
                              _ptr(distribution), _ptr(out), _ptr(workspace),
