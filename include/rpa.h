@@ -4,8 +4,11 @@
  *
  * Every pointer is a device pointer; the library never synchronises the host
  * and never allocates device memory on the rpa_forward path (the caller
- * passes a workspace of rpa_workspace_size() bytes).  Calls are ordered on
- * the given HIP stream (a hipStream_t passed as void*; NULL = default stream).
+ * passes a workspace of rpa_workspace_size() bytes; its contents need no
+ * initialisation, and calls sharing one workspace must be ordered on one
+ * stream).  q, k, v, kv_cache and out must be 16-byte aligned.  Calls are
+ * ordered on the given HIP stream (a hipStream_t passed as void*; NULL =
+ * default stream).
  *
  * Reference interfaces replaced (paths relative to the vllm-torchtpu tree):
  *   rpa_forward          <- ragged_paged_attention(...)
@@ -130,9 +133,10 @@ int rpa_kv_cache_update(const rpa_desc* d, const void* keys, const void* values,
                         const int32_t* page_indices, const int32_t* cu_q_lens,
                         const int32_t* distribution, void* stream);
 
-/* Full RPA call: cache update (unless skip_kv_update) followed by attention
- * for sequences [0, distribution[2]).  Output rows >= cu_q_lens[num_seqs]
- * are left untouched. */
+/* Full RPA call: cache update (unless skip_kv_update) and attention for
+ * sequences [0, distribution[2]); attention reads this call's new tokens from
+ * k/v (as the Pallas kernel does, kernel.py:634-641), or from the cache when
+ * skip_kv_update.  Output rows >= cu_q_lens[num_seqs] are left untouched. */
 int rpa_forward(const rpa_desc* d, const void* queries, const void* keys,
                 const void* values, void* kv_cache, const int32_t* kv_lens,
                 const int32_t* page_indices, const int32_t* cu_q_lens,

@@ -291,9 +291,9 @@ def test_decode_f32_out(gpu_device):
                           kv_dtype=torch.float32, seed=35, name="decode-f32"), gpu_device)
 
 
-def test_decode_repeated_calls_reset_counters(gpu_device):
-    """The split-merge arrival counters live in a persistent workspace; every call
-    must leave them at zero, so back-to-back calls stay correct."""
+def test_decode_repeated_calls(gpu_device):
+    """The decode partials live in a persistent per-device workspace; back-to-back
+    calls (and a different batch afterwards) must not see each other's partials."""
     w = W.make_workload([(1, k) for k in (4000, 33, 2048, 700, 1)], 32, 8, 128, 16, seed=36,
                         name="decode-repeat")
     exp_out, exp_cache = O.ref_ragged_paged_attention(*w.args(), mode="fp32", **w.kwargs)

@@ -47,12 +47,20 @@ rpa::Params make_params(const rpa_desc* d) {
   p.score_scale = d->sm_scale * d->k_scale * d->q_scale;
   p.v_scale = d->v_scale;
   p.rec = static_cast<int64_t>(d->kv_heads_x2) * d->head_dim_padded;
+  p.skip_kv_update = d->skip_kv_update ? 1 : 0;
+  p.decode_waves = 0;
   return p;
 }
 
-bool use_decode_path(const rpa_desc* d, const rpa::Params& p) {
+// Launch structure of a call.  The fused path is the decode kernel (when
+// the shape allows it) followed by the finish kernel; the generic path is the
+// KV-page write followed by the shape-generic attention kernel.
+bool use_fused_path(const rpa_desc* d, const rpa::Params& p) {
   return d->path != RPA_PATH_GENERIC &&
-         rpa::decode_supported(p, d->q_dtype, d->kv_dtype, d->out_dtype);
+         rpa::finish_supported(p, d->q_dtype, d->kv_dtype, d->out_dtype);
+}
+bool use_decode_kernel(const rpa_desc* d, const rpa::Params& p) {
+  return use_fused_path(d, p) && rpa::decode_supported(p, d->q_dtype, d->kv_dtype, d->out_dtype);
 }
 
 // Compute units of the current device (cached per device id).
@@ -130,7 +138,7 @@ size_t rpa_workspace_size(const rpa_desc* d) {
   if (rpa_validate_desc(d) != RPA_OK) return 0;
   const rpa::Params p = make_params(d);
   size_t bytes = 256;
-  if (use_decode_path(d, p)) bytes += rpa::decode_workspace_bytes(p, dtype_bytes(d->kv_dtype));
+  if (use_decode_kernel(d, p)) bytes += rpa::decode_workspace_bytes(p);
   return bytes;
 }
 
@@ -159,26 +167,38 @@ int rpa_forward(const rpa_desc* d, const void* queries, const void* keys, const 
   if (!queries || !kv_cache || !kv_lens || !page_indices || !cu_q_lens || !distribution || !out)
     return RPA_ERR_NULL_PTR;
   if (workspace_bytes < rpa_workspace_size(d) || workspace == nullptr) return RPA_ERR_WORKSPACE;
+  if (!d->skip_kv_update && (!keys || !values)) return RPA_ERR_NULL_PTR;
+  // Every kernel reads and writes 8- or 16-byte pieces.
+  const uintptr_t align = reinterpret_cast<uintptr_t>(queries) | reinterpret_cast<uintptr_t>(kv_cache) |
+                          reinterpret_cast<uintptr_t>(out) | reinterpret_cast<uintptr_t>(keys) |
+                          reinterpret_cast<uintptr_t>(values);
+  if (align & 15u) return RPA_ERR_INVALID_ARG;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  const rpa::Params p = make_params(d);
-  if (!d->skip_kv_update) {
-    if (!keys || !values) return RPA_ERR_NULL_PTR;
-    hipError_t e = rpa::launch_kv_update(p, dtype_bytes(d->kv_dtype), keys, values, kv_cache,
-                                         kv_lens, page_indices, cu_q_lens, distribution, s);
-    if (e != hipSuccess) return RPA_ERR_LAUNCH;
+  rpa::Params p = make_params(d);
+  if (!use_fused_path(d, p)) {
+    if (!d->skip_kv_update) {
+      hipError_t e = rpa::launch_kv_update(p, dtype_bytes(d->kv_dtype), keys, values, kv_cache,
+                                           kv_lens, page_indices, cu_q_lens, distribution, s);
+      if (e != hipSuccess) return RPA_ERR_LAUNCH;
+    }
+    hipError_t e = rpa::launch_attn_generic(p, d->q_dtype, d->kv_dtype, d->out_dtype, queries,
+                                            kv_cache, kv_lens, page_indices, cu_q_lens,
+                                            distribution, out, s);
+    return e == hipSuccess ? RPA_OK : RPA_ERR_LAUNCH;
   }
-  rpa::Params pg = p;
-  if (use_decode_path(d, p)) {
-    const rpa::DecodeWorkspace ws = rpa::carve_decode_workspace(p, workspace, dtype_bytes(d->kv_dtype));
-    hipError_t e = rpa::launch_decode(p, d->q_dtype, d->kv_dtype, d->out_dtype, ws, queries,
+  const int cus = current_num_cus();
+  rpa::DecodeWorkspace ws{nullptr, nullptr, 0};
+  if (use_decode_kernel(d, p)) {
+    p.decode_waves = rpa::decode_waves(p, cus);
+    ws = rpa::carve_decode_workspace(p, workspace);
+    hipError_t e = rpa::launch_decode(p, d->kv_dtype, d->out_dtype, ws, queries, keys, values,
                                       kv_cache, kv_lens, page_indices, cu_q_lens, distribution,
-                                      out, current_num_cus(), s);
+                                      out, s);
     if (e != hipSuccess) return RPA_ERR_LAUNCH;
-    pg.skip_decode_rows = 1;
   }
-  hipError_t e = rpa::launch_attn_generic(pg, d->q_dtype, d->kv_dtype, d->out_dtype, queries,
-                                          kv_cache, kv_lens, page_indices, cu_q_lens,
-                                          distribution, out, s);
+  hipError_t e = rpa::launch_finish(p, d->kv_dtype, d->out_dtype, ws, queries, keys, values,
+                                    kv_cache, kv_lens, page_indices, cu_q_lens, distribution, out,
+                                    cus, s);
   return e == hipSuccess ? RPA_OK : RPA_ERR_LAUNCH;
 }
 

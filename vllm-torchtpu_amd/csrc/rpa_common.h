@@ -32,7 +32,8 @@ struct Params {
   float score_scale;  // sm_scale * k_scale * q_scale
   float v_scale;
   int64_t rec;  // elements per token record = Kx2 * Dp
-  int32_t skip_decode_rows;  // generic path: leave single-token rows to the decode path
+  int32_t skip_kv_update;  // new tokens are already in the cache (read them from there)
+  int32_t decode_waves;    // wavefronts of the decode kernel's persistent grid (0: no decode kernel)
 };
 
 // ---------------------------------------------------------------------------
@@ -141,6 +142,14 @@ __device__ __forceinline__ float warp_sum(float v) {
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
   return v;
+}
+
+// Orders a wavefront's own LDS writes before its later LDS reads (and
+// reads before later writes) without a workgroup barrier.
+__device__ __forceinline__ void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
 // logit transform shared by every attention kernel: scale then soft cap

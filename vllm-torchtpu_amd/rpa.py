@@ -272,9 +272,8 @@ def _require_device(*tensors: torch.Tensor) -> torch.device:
     return dev
 
 
-# Per-device workspace, zero-initialised once.  The decode path keeps arrival
-# counters in it that every call leaves at zero again, so calls that share a
-# device's workspace must be ordered on one stream (as vLLM's are).
+# Per-device workspace (decode partials), grown on demand and kept.  Calls that
+# share a device's workspace must be ordered on one stream (as vLLM's are).
 _WORKSPACES: dict = {}
 
 
@@ -282,7 +281,7 @@ def _workspace(device: torch.device, nbytes: int) -> torch.Tensor:
     key = device.index if device.index is not None else torch.cuda.current_device()
     buf = _WORKSPACES.get(key)
     if buf is None or buf.numel() < nbytes:
-        buf = torch.zeros(max(nbytes, 1), dtype=torch.uint8, device=device)
+        buf = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=device)
         _WORKSPACES[key] = buf
     return buf
 
