@@ -48,6 +48,9 @@ rpa::Params make_params(const rpa_desc* d) {
   p.v_scale = d->v_scale;
   p.rec = static_cast<int64_t>(d->kv_heads_x2) * d->head_dim_padded;
   p.skip_kv_update = d->skip_kv_update ? 1 : 0;
+  p.ps_shift = -1;
+  for (int sh = 0; sh < 31; ++sh)
+    if ((1 << sh) == d->page_size) p.ps_shift = sh;
   p.decode_waves = 0;
   return p;
 }
@@ -187,7 +190,7 @@ int rpa_forward(const rpa_desc* d, const void* queries, const void* keys, const 
     return e == hipSuccess ? RPA_OK : RPA_ERR_LAUNCH;
   }
   const int cus = current_num_cus();
-  rpa::DecodeWorkspace ws{nullptr, nullptr, 0};
+  rpa::DecodeWorkspace ws{nullptr, nullptr, nullptr, 0};
   if (use_decode_kernel(d, p)) {
     p.decode_waves = rpa::decode_waves(p, cus);
     ws = rpa::carve_decode_workspace(p, workspace);

@@ -32,9 +32,19 @@ struct Params {
   float score_scale;  // sm_scale * k_scale * q_scale
   float v_scale;
   int64_t rec;  // elements per token record = Kx2 * Dp
+  int32_t ps_shift;        // log2(ps) when ps is a power of two, else -1
   int32_t skip_kv_update;  // new tokens are already in the cache (read them from there)
   int32_t decode_waves;    // wavefronts of the decode kernel's persistent grid (0: no decode kernel)
 };
+
+// Page and slot of logical position j (>= 0): shifts for power-of-two page
+// sizes (a wavefront-uniform branch), division otherwise.
+__device__ __forceinline__ int32_t page_of(const Params& p, int32_t j) {
+  return p.ps_shift >= 0 ? (j >> p.ps_shift) : j / p.ps;
+}
+__device__ __forceinline__ int32_t slot_of(const Params& p, int32_t j) {
+  return p.ps_shift >= 0 ? (j & (p.ps - 1)) : j % p.ps;
+}
 
 // ---------------------------------------------------------------------------
 // Scalar conversions, written from the format definitions.

@@ -216,9 +216,9 @@ __device__ __forceinline__ void write_new_token(const Params& p, typename KV::st
   using E = typename KV::storage;
   constexpr int EPP = 8 / sizeof(E);             // elements per 8-byte piece
   constexpr int PIECES = DP / EPP;               // pieces per head chunk
-  const int32_t pg = page_indices[static_cast<int64_t>(s) * p.pps + j / p.ps];
+  const int32_t pg = page_indices[static_cast<int64_t>(s) * p.pps + page_of(p, j)];
   if (pg < 0 || pg >= p.P) return;
-  E* rec = cache + (static_cast<int64_t>(pg) * p.ps + j % p.ps) * p.rec;
+  E* rec = cache + (static_cast<int64_t>(pg) * p.ps + slot_of(p, j)) * p.rec;
   const int64_t src = (static_cast<int64_t>(tq) * p.Hkv + h) * p.D;
   for (int i = lane; i < 2 * PIECES; i += 64) {
     const int c = i / PIECES, e0 = (i % PIECES) * EPP;
@@ -244,7 +244,8 @@ decode_kernel(Params p, const uint16_t* __restrict__ q, const typename KV::stora
               typename KV::storage* __restrict__ cache, const int32_t* __restrict__ kv_lens,
               const int32_t* __restrict__ page_indices, const int32_t* __restrict__ cu,
               const int32_t* __restrict__ dist, OutS* __restrict__ out,
-              float* __restrict__ part_o, float* __restrict__ part_ml, int32_t max_units) {
+              float* __restrict__ part_o, float* __restrict__ part_ml,
+              int32_t* __restrict__ plan_ws, int32_t max_units) {
   using C = DecodeCfg<KV, DP>;
   constexpr int TT = C::TT, NOCT = C::NOCT, NPART = C::NPART, NG = C::NG;
   constexpr int KP = NPART / 2;        // K parts (then V parts)
@@ -253,7 +254,7 @@ decode_kernel(Params p, const uint16_t* __restrict__ q, const typename KV::stora
   constexpr int NT = DP / 16;          // PV output tiles over head_dim
 
   __shared__ __align__(16) unsigned char smem[kWaves * C::WAVE_LDS];
-  __shared__ PlanLds L;
+  __shared__ PlanCore L;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -263,7 +264,8 @@ decode_kernel(Params p, const uint16_t* __restrict__ q, const typename KV::stora
   const int tl = lane >> 3;  // load shape: token within the octet
   const int ol = lane & 7;   // load shape: 16-byte column within a 128-byte part
 
-  const Plan pl = build_plan(p, kv_lens, cu, dist, TT, max_units, true, L);
+  const Plan pl = build_plan(p, kv_lens, cu, dist, TT, max_units, true, L, nullptr);
+  publish_plan(p, pl, L, cu, plan_ws);
   const int32_t total_items = pl.total_units * p.Hkv;
   const int32_t gw = static_cast<int32_t>(blockIdx.x) * kWaves + wave;
   const int32_t nw = static_cast<int32_t>(gridDim.x) * kWaves;
@@ -283,11 +285,12 @@ decode_kernel(Params p, const uint16_t* __restrict__ q, const typename KV::stora
     ti.h = uni(unit - pu * p.Hkv);
     ti.s = uni(find_prefix(L.units, pl.num_seqs, pu));
     const int32_t u = uni(pu - L.units[ti.s]);
-    ti.nt = uni(L.nt[ti.s]);
+    const int32_t dkv = uni(L.dkv[ti.s]);
+    ti.nt = decode_tiles(p, dkv, TT);
     ti.lt = u * pl.tpu;
     ti.lt_end = min(ti.nt, ti.lt + pl.tpu);
     int32_t lo, hi;
-    decode_range(p, L.kvlen[ti.s], &lo, &hi);
+    decode_range(p, dkv, &lo, &hi);
     ti.lo = uni(lo);
     ti.hi = uni(hi);
     return ti;
@@ -316,7 +319,7 @@ decode_kernel(Params p, const uint16_t* __restrict__ q, const typename KV::stora
     const int32_t* ptab = page_indices + static_cast<int64_t>(sq) * p.pps;
     const int32_t base = ti.lo + ti.lt * TT;
 #pragma unroll
-    for (int o = 0; o < NOCT; ++o) pp.pg[o] = ptab[clamp_tok(ti, base + 8 * o + tl) / p.ps];
+    for (int o = 0; o < NOCT; ++o) pp.pg[o] = ptab[page_of(p, clamp_tok(ti, base + 8 * o + tl))];
   };
   // Tile loads: octet o, part pt -> bytes [128pt + 16ol, +16) of the head's
   // K|V chunk of that token.
@@ -328,7 +331,7 @@ decode_kernel(Params p, const uint16_t* __restrict__ q, const typename KV::stora
       const int32_t c = clamp_tok(ti, base + 8 * o + tl);
       const int32_t pg = min(max(pp.pg[o], 0), p.P - 1);
       const unsigned char* rec = reinterpret_cast<const unsigned char*>(
-          cache + (static_cast<int64_t>(pg) * p.ps + c % p.ps) * p.rec +
+          cache + (static_cast<int64_t>(pg) * p.ps + slot_of(p, c)) * p.rec +
           static_cast<int64_t>(2 * ti.h) * DP);
 #pragma unroll
       for (int pt = 0; pt < NPART; ++pt)
@@ -556,12 +559,14 @@ hipError_t launch_typed(const Params& p, const DecodeWorkspace& ws, const void* 
     hipLaunchKernelGGL((decode_kernel<KV, DP, OutS, true>), grid, block, 0, stream, p,
                        static_cast<const uint16_t*>(q), static_cast<const E*>(k),
                        static_cast<const E*>(v), static_cast<E*>(cache), kv_lens, page_indices,
-                       cu, dist, static_cast<OutS*>(out), ws.part_o, ws.part_ml, ws.max_units);
+                       cu, dist, static_cast<OutS*>(out), ws.part_o, ws.part_ml, ws.plan,
+                       ws.max_units);
   } else {
     hipLaunchKernelGGL((decode_kernel<KV, DP, OutS, false>), grid, block, 0, stream, p,
                        static_cast<const uint16_t*>(q), static_cast<const E*>(k),
                        static_cast<const E*>(v), static_cast<E*>(cache), kv_lens, page_indices,
-                       cu, dist, static_cast<OutS*>(out), ws.part_o, ws.part_ml, ws.max_units);
+                       cu, dist, static_cast<OutS*>(out), ws.part_o, ws.part_ml, ws.plan,
+                       ws.max_units);
   }
   return hipGetLastError();
 }
@@ -634,12 +639,15 @@ static int32_t decode_max_units(const Params& p) {
   return static_cast<int32_t>(m);
 }
 
+// Workspace layout: the partials, then the published plan.  Nothing in it
+// needs initialising.
 size_t decode_workspace_bytes(const Params& p) {
   const int64_t rows = decode_slot_rows(p.qpk);
   const int64_t slots = static_cast<int64_t>(decode_max_units(p)) * p.Hkv;
   size_t bytes = 256;
   bytes += static_cast<size_t>(slots) * rows * p.Dp * sizeof(float);  // part_o
   bytes += static_cast<size_t>(slots) * rows * 2 * sizeof(float);     // part_ml
+  bytes += static_cast<size_t>(plan_ints(p.S, p.T)) * sizeof(int32_t);  // plan
   return bytes;
 }
 
@@ -652,6 +660,8 @@ DecodeWorkspace carve_decode_workspace(const Params& p, void* base) {
   ws.part_o = reinterpret_cast<float*>(ptr);
   ptr += static_cast<size_t>(slots) * rows * p.Dp * sizeof(float);
   ws.part_ml = reinterpret_cast<float*>(ptr);
+  ptr += static_cast<size_t>(slots) * rows * 2 * sizeof(float);
+  ws.plan = reinterpret_cast<int32_t*>(ptr);
   return ws;
 }
 

@@ -41,9 +41,9 @@ __device__ __forceinline__ KeySource key_source(const Params& p, const int32_t* 
     ks.v_off = ks.k_off;
     ks.from_input = 1;
   } else {
-    int32_t page = ptab[j / p.ps];
+    int32_t page = ptab[page_of(p, j)];
     page = min(max(page, 0), p.P - 1);
-    const int64_t rec_base = (static_cast<int64_t>(page) * p.ps + (j % p.ps)) * p.rec;
+    const int64_t rec_base = (static_cast<int64_t>(page) * p.ps + slot_of(p, j)) * p.rec;
     ks.k_off = rec_base + static_cast<int64_t>(2 * h) * p.Dp;
     ks.v_off = ks.k_off + p.Dp;
     ks.from_input = 0;
@@ -119,6 +119,34 @@ __device__ __forceinline__ void generic_row(const Params& p, const float* qs,
   for (int c = 0; c < kGenericMaxChunks; ++c) {
     const int d = lane + 64 * c;
     if (d < p.D) store_out(orow, d, acc[c] * inv_l);
+  }
+}
+
+// New K/V record of token row t (logical position j of sequence s) into its
+// cache page: merge_kv(k, v)[t] (kernel.py:1140-1168) -- combined head 2h is
+// K_h, 2h + 1 is V_h, heads >= 2 Hkv and dims >= D are zero.  Bits are
+// copied as they are.  8-byte pieces (D * element bytes is a multiple of 8).
+template <typename E>
+__device__ __forceinline__ void write_record(const Params& p, E* __restrict__ cache,
+                                             const int32_t* __restrict__ page_indices,
+                                             const E* __restrict__ keys,
+                                             const E* __restrict__ values, int32_t s, int32_t j,
+                                             int32_t t, int lane) {
+  constexpr int EPP = 8 / sizeof(E);
+  const int32_t pg = page_indices[static_cast<int64_t>(s) * p.pps + page_of(p, j)];
+  if (pg < 0 || pg >= p.P) return;
+  E* rec = cache + (static_cast<int64_t>(pg) * p.ps + slot_of(p, j)) * p.rec;
+  const int64_t src_row = static_cast<int64_t>(t) * p.Hkv * p.D;
+  const int32_t per_head = p.Dp / EPP;
+  const int32_t pieces = p.Kx2 * per_head;
+  for (int32_t i = lane; i < pieces; i += 64) {
+    const int32_t c = i / per_head;
+    const int32_t e0 = (i - c * per_head) * EPP;
+    uint2 v = make_uint2(0u, 0u);
+    if (c < 2 * p.Hkv && e0 < p.D)
+      v = *reinterpret_cast<const uint2*>(((c & 1) ? values : keys) + src_row +
+                                          static_cast<int64_t>(c >> 1) * p.D + e0);
+    *reinterpret_cast<uint2*>(rec + static_cast<int64_t>(c) * p.Dp + e0) = v;
   }
 }
 

@@ -22,8 +22,35 @@ constexpr int kMaxDecodeSeqs = 2048;
 struct DecodeWorkspace {
   float* part_o;      // [max_units * Hkv][rows][Dp] un-normalised partial outputs
   float* part_ml;     // [max_units * Hkv][rows][2] (row max in log2 units, row sum)
+  int32_t* plan;      // the decode kernel's plan for the finish kernel (layout below)
   int32_t max_units;  // capacity in (sequence, unit) pairs
 };
+
+
+// Plan written by the decode kernel: [0] num_seqs n, [1] tiles per unit,
+// [2] total units, [3] unused; units[S + 1] (exclusive prefix, units[n] =
+// total), dkv[S] (kv_len of a decode sequence, else 0), tq[S] (q row of the
+// sequence), rowseq[T] (sequence of a token row the finish kernel owns, -1 for
+// decode rows and padding rows).
+struct PlanView {
+  const int32_t* hdr;
+  const int32_t* units;
+  const int32_t* dkv;
+  const int32_t* tq;
+  const int32_t* rowseq;
+};
+__host__ __device__ inline PlanView plan_view(const int32_t* plan, int32_t S) {
+  PlanView v;
+  v.hdr = plan;
+  v.units = plan + 4;
+  v.dkv = v.units + (S + 1);
+  v.tq = v.dkv + S;
+  v.rowseq = v.tq + S;
+  return v;
+}
+__host__ __device__ inline int64_t plan_ints(int32_t S, int32_t T) {
+  return 4 + (S + 1) + 2 * static_cast<int64_t>(S) + S + T;
+}
 
 bool decode_supported(const Params& p, int q_dtype, int kv_dtype, int out_dtype);
 int decode_waves(const Params& p, int num_cus);

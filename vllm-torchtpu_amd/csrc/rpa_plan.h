@@ -29,16 +29,25 @@ struct Plan {
   int32_t num_seqs;     // min(distribution[2], S)
   int32_t tpu;          // tiles per unit
   int32_t total_units;  // (sequence, unit) pairs over all decode sequences
+  int32_t n_other;      // sequences with rows that are not decode rows
+  int32_t cu_end;       // cu_q_lens[num_seqs]
 };
 
-// Per-sequence plan arrays in LDS (kMaxDecodeSeqs entries each).
-struct PlanLds {
-  int32_t nt[kMaxDecodeSeqs];         // decode tiles (0: not a decode sequence)
-  int32_t units[kMaxDecodeSeqs + 1];  // exclusive prefix of units; units[n] = total
+// Per-sequence plan arrays in LDS (kMaxDecodeSeqs entries each).  The
+// decode kernel needs only the core; the finish kernel also keeps every
+// sequence's kv_len and cu_q_lens.
+template <int N>
+struct PlanCoreT {
+  static constexpr int kCap = N;  // sequences the plan holds
+  int32_t units[N + 1];  // exclusive prefix of units; units[n] = total
+  int32_t dkv[N];        // kv_len of a decode sequence (clamped), else 0
+  int32_t tq[N];         // q row of the sequence (cu_q_lens[s], clamped)
+  int32_t red[3 * kPlanWaves];
+};
+using PlanCore = PlanCoreT<kMaxDecodeSeqs>;
+struct PlanRows {
   int32_t kvlen[kMaxDecodeSeqs];      // kv_len clamped to the page table (every sequence)
-  int32_t tq[kMaxDecodeSeqs];         // q row of the sequence (cu_q_lens[s], clamped)
   int32_t cu[kMaxDecodeSeqs + 1];     // cu_q_lens[0 .. num_seqs]
-  int32_t red[2 * kPlanWaves];
 };
 
 __device__ __forceinline__ void decode_range(const Params& p, int32_t kv_len, int32_t* lo,
@@ -98,53 +107,109 @@ __device__ __forceinline__ int32_t plan_tiles_per_unit(int64_t total_tiles, int3
   return static_cast<int32_t>(tpu > need ? tpu : need);
 }
 
+// Tiles of a decode sequence with kv_len dkv (0 for a non-decode sequence).
+__device__ __forceinline__ int32_t decode_tiles(const Params& p, int32_t dkv, int32_t tile) {
+  if (dkv <= 0) return 0;
+  int32_t lo, hi;
+  decode_range(p, dkv, &lo, &hi);
+  return (hi - lo + tile - 1) / tile;
+}
+
 // Builds the plan in LDS (all threads of a kPlanThreads-wide workgroup take
 // part; ends with a barrier).  With decode_enabled false no sequence is a
-// decode sequence (every row belongs to the finish kernel).
+// decode sequence (every row belongs to the finish kernel).  R, when given,
+// receives every sequence's kv_len and cu_q_lens.
+template <typename PlanLds>
 __device__ __forceinline__ Plan build_plan(const Params& p, const int32_t* kv_lens,
                                            const int32_t* cu, const int32_t* dist, int32_t tile,
-                                           int32_t max_units, bool decode_enabled, PlanLds& L) {
+                                           int32_t max_units, bool decode_enabled, PlanLds& L,
+                                           PlanRows* R) {
   Plan pl;
   const int tid = threadIdx.x;
-  const int32_t n = num_seqs_of(dist, p.S);
+  const int32_t n = min(num_seqs_of(dist, p.S), PlanLds::kCap);
   pl.num_seqs = n;
-  int32_t tiles = 0, seqs = 0;
+  int32_t tiles = 0, seqs = 0, others = 0;
   for (int32_t s = tid; s < n; s += kPlanThreads) {
-    int32_t kl, lo, hi, nt = 0;
-    if (is_decode_seq(p, cu, kv_lens, s, &kl) && decode_enabled) {
-      decode_range(p, kl, &lo, &hi);
-      nt = (hi - lo + tile - 1) / tile;
-      seqs += 1;
-    }
-    L.kvlen[s] = kl;
+    int32_t kl;
+    const bool dec = is_decode_seq(p, cu, kv_lens, s, &kl) && decode_enabled;
+    const int32_t nt = dec ? decode_tiles(p, kl, tile) : 0;
+    seqs += dec ? 1 : 0;
+    others += (!dec && cu[s + 1] > cu[s]) ? 1 : 0;
+    L.dkv[s] = dec ? kl : 0;
     L.tq[s] = min(max(cu[s], 0), max(p.T - 1, 0));
-    L.cu[s] = cu[s];
-    L.nt[s] = nt;
+    L.units[s] = nt;  // tiles for now; turned into units below
+    if (R != nullptr) {
+      R->kvlen[s] = kl;
+      R->cu[s] = cu[s];
+    }
     tiles += nt;
   }
-  if (tid == 0) L.cu[n] = cu[n];
+  if (R != nullptr && tid == 0) R->cu[n] = cu[n];
   for (int o = 32; o > 0; o >>= 1) {
     tiles += __shfl_xor(tiles, o, 64);
     seqs += __shfl_xor(seqs, o, 64);
+    others += __shfl_xor(others, o, 64);
   }
   if ((tid & 63) == 0) {
     L.red[tid >> 6] = tiles;
     L.red[kPlanWaves + (tid >> 6)] = seqs;
+    L.red[2 * kPlanWaves + (tid >> 6)] = others;
   }
   __syncthreads();
   int64_t total_tiles = 0;
-  int32_t nseq = 0;
+  int32_t nseq = 0, nother = 0;
   for (int w = 0; w < kPlanWaves; ++w) {
     total_tiles += L.red[w];
     nseq += L.red[kPlanWaves + w];
+    nother += L.red[2 * kPlanWaves + w];
   }
+  pl.n_other = nother;
+  pl.cu_end = cu[n];
   __syncthreads();
   pl.tpu = plan_tiles_per_unit(total_tiles, nseq, p.Hkv, p.decode_waves, max_units);
-  for (int32_t s = tid; s < n; s += kPlanThreads) L.units[s] = (L.nt[s] + pl.tpu - 1) / pl.tpu;
+  for (int32_t s = tid; s < n; s += kPlanThreads) L.units[s] = (L.units[s] + pl.tpu - 1) / pl.tpu;
   __syncthreads();
   block_exclusive_scan(L.units, n, L.red);
   pl.total_units = L.units[n];
   return pl;
+}
+
+// Publishes the plan for the finish kernel (every thread of the workgroup
+// takes part; workgroup b writes the row map of sequences b, b + G, ...).
+template <typename PlanLds>
+__device__ __forceinline__ void publish_plan(const Params& p, const Plan& pl, const PlanLds& L,
+                                             const int32_t* cu, int32_t* plan) {
+  const PlanView v = plan_view(plan, p.S);
+  int32_t* units = const_cast<int32_t*>(v.units);
+  int32_t* dkv = const_cast<int32_t*>(v.dkv);
+  int32_t* tq = const_cast<int32_t*>(v.tq);
+  int32_t* rowseq = const_cast<int32_t*>(v.rowseq);
+  const int tid = threadIdx.x;
+  const int32_t n = pl.num_seqs;
+  if (blockIdx.x == 0) {
+    if (tid == 0) {
+      plan[0] = n;
+      plan[1] = pl.tpu;
+      plan[2] = pl.total_units;
+      plan[3] = 0;
+    }
+    for (int32_t s = tid; s <= n; s += kPlanThreads) units[s] = L.units[s];
+    for (int32_t s = tid; s < n; s += kPlanThreads) {
+      dkv[s] = L.dkv[s];
+      tq[s] = L.tq[s];
+    }
+  }
+  const int32_t G = static_cast<int32_t>(gridDim.x);
+  for (int32_t s = static_cast<int32_t>(blockIdx.x); s < n; s += G) {
+    const int32_t r0 = min(max(cu[s], 0), p.T), r1 = min(max(cu[s + 1], r0), p.T);
+    const int32_t val = L.dkv[s] > 0 ? -1 : s;
+    for (int32_t t = r0 + tid; t < r1; t += kPlanThreads) rowseq[t] = val;
+  }
+  // Padding rows.
+  const int32_t pad0 = min(max(cu[n], 0), p.T);
+  for (int32_t t = pad0 + static_cast<int32_t>(blockIdx.x) * kPlanThreads + tid; t < p.T;
+       t += G * kPlanThreads)
+    rowseq[t] = -1;
 }
 
 // Largest s in [0, n) with prefix[s] <= x.
@@ -167,9 +232,8 @@ __host__ __device__ constexpr int decode_slot_rows(int qpk) {
 }
 
 // Keys per tile: 16 KiB of one kv head's K|V bytes (16 x 16-byte loads per
-// lane); 32 keys at head_dim 128 bf16.
+// lane): 32 keys at head_dim 128 bf16, 64 for fp8.
 __host__ __device__ constexpr int decode_tile_tokens(int dp, int kv_bytes) {
   return 16384 / (2 * dp * kv_bytes);
 }
-
 }  // namespace rpa

@@ -272,8 +272,9 @@ def _require_device(*tensors: torch.Tensor) -> torch.device:
     return dev
 
 
-# Per-device workspace (decode partials), grown on demand and kept.  Calls that
-# share a device's workspace must be ordered on one stream (as vLLM's are).
+# Per-device workspace (decode partials and work plan), grown on demand and
+# kept.  Calls that share a device's workspace must be ordered on one stream
+# (as vLLM's are).
 _WORKSPACES: dict = {}
 
 
