@@ -11,14 +11,19 @@ Prints one JSON line:
   value      -- query tokens per second of whole calls (HIP-graph replay of the
                 call, so host launch overhead is not on the clock; the eager
                 figure is reported beside it)
-  roofline   -- the attention kernel's algorithmic HBM bytes per launch divided
-                by its average launch duration (HIP events around a graph of
-                attention-only launches on the launching stream), against
-                MI355X's 8 TB/s
+  roofline   -- the dominant kernel (the decode kernel when the batch has
+                decode rows, else the whole attention call): its algorithmic
+                HBM bytes per launch divided by its average launch duration
+                (HIP events on the launching stream around graph replays of
+                that kernel alone), against MI355X's 8 TB/s; `traffic` is the
+                measured HBM bytes per launch from the committed rocprofv3
+                FETCH_SIZE / WRITE_SIZE profile of this workload, scaled by the
+                copy-kernel calibration stored with it (null without one)
   cpu_baseline -- the CPU oracle (faithful restatement of the reference
                 ref_ragged_paged_attention) on the host cores, same workload
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--config 2]
+       python bench.py --copy-probe BYTES   (calibration kernel for rocprofv3 --pmc)
 """
 
 import argparse
@@ -55,8 +60,12 @@ def cpu_baseline(w, seconds):
 
     from oracle import rpa_oracle as O
 
-    threads = os.cpu_count() or 1
-    torch.set_num_threads(threads)
+    # The cores this process may use (the box's share, OMP_NUM_THREADS when
+    # set), not the whole machine's count.
+    threads = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else 1
+    if os.environ.get("OMP_NUM_THREADS", "").isdigit():
+        threads = min(threads, int(os.environ["OMP_NUM_THREADS"]))
+    torch.set_num_threads(max(threads, 1))
     model = "unknown"
     try:
         for line in open("/proc/cpuinfo"):
@@ -84,6 +93,43 @@ def cpu_baseline(w, seconds):
     }
 
 
+def copy_probe(nbytes, reps):
+    """A plain device copy of `nbytes` (src -> dst), `reps` times: the
+    reference kernel whose FETCH_SIZE / WRITE_SIZE per dispatch calibrates the
+    counters (it moves exactly nbytes in and nbytes out)."""
+    import torch
+
+    dev = torch.device("cuda:0")
+    n = nbytes // 16
+    src = torch.ones(n, 4, dtype=torch.int32, device=dev)
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        dst.copy_(src)
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / reps
+    print(json.dumps({"copy_probe_bytes": n * 16, "reps": reps, "ms": round(ms, 5),
+                      "gbps_read_plus_write": round(2 * n * 16 / (ms * 1e-3) / 1e9, 1)}),
+          flush=True)
+
+
+def load_traffic(config, kernel):
+    """HBM bytes per launch of `kernel` on config `config` from the committed
+    counter profile (profiles/pmc_<kernel>_c<config>.json), or None."""
+    path = os.path.join(ROOT, "profiles", f"pmc_{kernel}_c{config}.json")
+    if not os.path.exists(path):
+        return None
+    try:
+        with open(path) as f:
+            d = json.load(f)
+        return int(d["traffic_bytes_per_launch"])
+    except (OSError, ValueError, KeyError):
+        return None
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -93,6 +139,7 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-graph", action="store_true")
+    ap.add_argument("--copy-probe", type=int, default=0, metavar="BYTES")
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -102,12 +149,15 @@ def main():
               "single MI355X's throughput is the measured figure; multi-GPU runs are not part "
               "of this build.", file=sys.stderr)
         sys.exit(2)
+    if args.copy_probe:
+        copy_probe(args.copy_probe, max(args.steps, 1))
+        return
 
     import torch
 
     import vllm_torchtpu_amd as R
     import vllm_torchtpu_amd.workloads as W
-    from vllm_torchtpu_amd.util import cdiv
+    from vllm_torchtpu_amd import _native as N
 
     dev = torch.device("cuda:0")
     _log(f"building workload C{args.config}")
@@ -121,6 +171,23 @@ def main():
 
     def attn_only():
         return R.ragged_paged_attention(*g.args(), skip_kv_update=True, **kw)
+
+    k_out = torch.empty(g.q.shape, dtype=g.q.dtype, device=dev)
+
+    def decode_only():
+        return R.rpa._rpa_forward_impl(
+            *g.args(), k_out, use_causal_mask=kw.get("use_causal_mask", True),
+            skip_kv_update=True, sm_scale=kw["sm_scale"],
+            sliding_window=kw.get("sliding_window"), soft_cap=kw.get("soft_cap"),
+            q_scale=kw.get("q_scale"), k_scale=kw.get("k_scale"), v_scale=kw.get("v_scale"),
+            path=N.RPA_PATH_DECODE_ONLY)
+
+    has_decode = True
+    try:
+        decode_only()
+    except (NotImplementedError, ValueError, RuntimeError) as e:
+        _log(f"decode kernel does not apply ({e}); timing the whole attention call")
+        has_decode = False
 
     _log("warm-up")
     for _ in range(args.warmup):
@@ -136,50 +203,52 @@ def main():
     torch.cuda.synchronize()
     eager_s = time.perf_counter() - t0
 
-    graph_s = None
-    attn_ms = None
-    if not args.no_graph:
-        _log("capturing HIP graphs")
-        s = torch.cuda.Stream(dev)
-        s.wait_stream(torch.cuda.current_stream(dev))
-        with torch.cuda.stream(s):
-            for _ in range(2):
-                step()
-                attn_only()
-        torch.cuda.current_stream(dev).wait_stream(s)
-        torch.cuda.synchronize()
-        g_step = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(g_step):
-            step()
-        g_attn = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(g_attn):
-            attn_only()
-        for _ in range(3):
-            g_step.replay()
-            g_attn.replay()
-        torch.cuda.synchronize()
-        _log(f"timing {args.steps} graph steps")
-        t0 = time.perf_counter()
-        for _ in range(args.steps):
-            g_step.replay()
-        torch.cuda.synchronize()
-        graph_s = time.perf_counter() - t0
-        # Attention kernel alone, HIP events on the replay stream.
+    def replay_ms(graph):
+        # HIP events on the current stream, which the replays launch on.
         e0 = torch.cuda.Event(enable_timing=True)
         e1 = torch.cuda.Event(enable_timing=True)
         e0.record()
         for _ in range(args.steps):
-            g_attn.replay()
+            graph.replay()
         e1.record()
         torch.cuda.synchronize()
-        attn_ms = e0.elapsed_time(e1) / args.steps
+        return e0.elapsed_time(e1) / args.steps
+
+    graph_s = attn_ms = kern_ms = None
+    if not args.no_graph:
+        _log("capturing HIP graphs")
+        fns = [step, attn_only] + ([decode_only] if has_decode else [])
+        s = torch.cuda.Stream(dev)
+        s.wait_stream(torch.cuda.current_stream(dev))
+        with torch.cuda.stream(s):
+            for _ in range(2):
+                for fn in fns:
+                    fn()
+        torch.cuda.current_stream(dev).wait_stream(s)
+        torch.cuda.synchronize()
+        graphs = []
+        for fn in fns:
+            gr = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(gr):
+                fn()
+            graphs.append(gr)
+        for _ in range(3):
+            for gr in graphs:
+                gr.replay()
+        torch.cuda.synchronize()
+        _log(f"timing {args.steps} graph steps")
+        t0 = time.perf_counter()
+        for _ in range(args.steps):
+            graphs[0].replay()
+        torch.cuda.synchronize()
+        graph_s = time.perf_counter() - t0
+        attn_ms = replay_ms(graphs[1])
+        kern_ms = replay_ms(graphs[2]) if has_decode else attn_ms
 
     timed_s = graph_s if graph_s is not None else eager_s
     tokens = w.num_tokens
     value = tokens * args.steps / timed_s
     ms_per_step = timed_s / args.steps * 1e3
-
-    from oracle import rpa_oracle as O  # byte/flop formulas only
 
     kvl = w.kv_lens.tolist()
     cu = w.cu_q_lens.tolist()
@@ -190,20 +259,25 @@ def main():
     kvb = w.kv_cache.element_size()
     qb = w.q.element_size()
     win = kw.get("sliding_window")
-    call_bytes = O.algorithmic_bytes(kvl, cu, n, hq, hkv, d, dp, ps, qb, kvb, qb,
+    call_bytes = W.algorithmic_bytes(kvl, cu, n, hq, hkv, d, dp, ps, qb, kvb, qb,
                                      sliding_window=win)
-    # Attention-only launch: no new-KV write.
-    newkv = sum((cu[i + 1] - cu[i]) * 2 * hkv * dp * kvb for i in range(n))
-    attn_bytes = call_bytes - newkv
-    flops = O.algorithmic_flops(kvl, cu, n, hq, d, sliding_window=win)
+    attn_bytes = W.algorithmic_bytes(kvl, cu, n, hq, hkv, d, dp, ps, qb, kvb, qb,
+                                     sliding_window=win, kv_write=False)
+    dec_bytes = W.decode_kernel_bytes(kvl, cu, n, hq, hkv, d, dp, ps, qb, kvb,
+                                      sliding_window=win)
+    flops = W.prefill_flops(kvl, cu, n, hq, d, sliding_window=win)
 
     roofline = None
-    if attn_ms is not None:
-        achieved = attn_bytes / (attn_ms * 1e-3) / 1e9
+    if kern_ms is not None:
+        kernel = "decode_kernel" if has_decode else "attention_call"
+        kbytes = dec_bytes if has_decode else attn_bytes
+        achieved = kbytes / (kern_ms * 1e-3) / 1e9
         roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS,
                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4),
-                    "traffic": None, "kernel_ms": round(attn_ms, 5),
-                    "bytes_per_launch": attn_bytes}
+                    "traffic": load_traffic(args.config, kernel), "kernel": kernel,
+                    "kernel_ms": round(kern_ms, 5), "bytes_per_launch": kbytes,
+                    "attention_call_ms": round(attn_ms, 5),
+                    "attention_call_bytes": attn_bytes}
 
     cpu = None
     if not args.no_cpu_baseline:

@@ -61,6 +61,12 @@ typedef enum rpa_status {
 typedef enum rpa_path {
   RPA_PATH_AUTO = 0,    /* pick the fastest implementation for the shape       */
   RPA_PATH_GENERIC = 1, /* force the shape-generic wave-per-row implementation */
+  /* Measurement only: launch the decode kernel alone (the kernel the
+   * benchmark's roofline times).  Outputs of decode rows whose key range is
+   * split over several units, and every non-decode row, are left unfinished;
+   * RPA_ERR_UNSUPPORTED when the decode kernel does not take the descriptor's
+   * dtypes or extents (which rows are decode rows is decided on the device). */
+  RPA_PATH_DECODE_ONLY = 2,
 } rpa_path;
 
 /* Plain-old-data descriptor of one call.  Shapes follow kernel.py:1609-1631:

@@ -442,39 +442,5 @@ def ref_ragged_paged_attention(
     return result, work.view(kv_dtype)
 
 
-def algorithmic_bytes(kv_lens, cu_q_lens, num_seqs, hq, hkv, d, dp, page_size,
-                      q_bytes, kv_bytes, out_bytes, sliding_window=None):
-    """Algorithmic HBM bytes of one RPA call (the formula the bench reports).
-
-    KV read of R_s tokens, new-KV write, Q read, O write, page-table and
-    metadata reads.
-    """
-    total = 0
-    for s in range(num_seqs):
-        q_len = int(cu_q_lens[s + 1]) - int(cu_q_lens[s])
-        kv_len = int(kv_lens[s])
-        r = kv_len if sliding_window is None else min(kv_len, q_len + sliding_window - 1)
-        total += r * 2 * hkv * dp * kv_bytes
-        total += q_len * 2 * hkv * dp * kv_bytes
-        total += q_len * hq * d * (q_bytes + out_bytes)
-        total += cdiv(kv_len, page_size) * 4
-    total += (3 * num_seqs + 4) * 4
-    return total
-
-
-def algorithmic_flops(kv_lens, cu_q_lens, num_seqs, hq, d, sliding_window=None):
-    """4 * D * Hq * sum over q rows of attended keys."""
-    tot = 0
-    for s in range(num_seqs):
-        q_len = int(cu_q_lens[s + 1]) - int(cu_q_lens[s])
-        kv_len = int(kv_lens[s])
-        for i in range(q_len):
-            a = kv_len - q_len + i + 1
-            if sliding_window is not None:
-                a = min(a, sliding_window)
-            tot += a
-    return 4 * d * hq * tot
-
-
 def _self_check():  # pragma: no cover - manual use
     print(get_kv_cache_shape(4, 16, 2, 128, torch.bfloat16), math.pi)

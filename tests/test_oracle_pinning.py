@@ -400,11 +400,19 @@ def test_dynamic_validation_raises(idx):
 
 def test_algorithmic_bytes_formula():
     """Closed-form byte count on a hand-computed case."""
+    import vllm_torchtpu_amd.workloads as WL
+
     kvl, cu = [100, 7], [0, 1, 4]
-    b = O.algorithmic_bytes(kvl, cu, 2, 8, 2, 128, 128, 16, 2, 2, 2)
+    b = WL.algorithmic_bytes(kvl, cu, 2, 8, 2, 128, 128, 16, 2, 2, 2)
     rec = 2 * 2 * 128 * 2
     expect = (100 + 7) * rec + 4 * rec + 4 * 8 * 128 * 4 + (7 + 1) * 4 + (3 * 2 + 4) * 4
     assert b == expect
-    assert O.algorithmic_flops(kvl, cu, 2, 8, 128) == 4 * 128 * 8 * (100 + 5 + 6 + 7)
-    assert math.isclose(O.algorithmic_flops([10], [0, 4], 1, 1, 1, sliding_window=8),
+    assert WL.algorithmic_bytes(kvl, cu, 2, 8, 2, 128, 128, 16, 2, 2, 2,
+                                kv_write=False) == expect - 4 * rec
+    # decode kernel: only sequence 0 (q_len 1) counts, q read only.
+    assert WL.decode_kernel_bytes(kvl, cu, 2, 8, 2, 128, 128, 16, 2, 2) == \
+        100 * rec + 8 * 128 * 2 + 7 * 4 + (3 * 2 + 4) * 4
+    assert WL.algorithmic_flops(kvl, cu, 2, 8, 128) == 4 * 128 * 8 * (100 + 5 + 6 + 7)
+    assert WL.prefill_flops(kvl, cu, 2, 8, 128) == 4 * 128 * 8 * (5 + 6 + 7)
+    assert math.isclose(WL.algorithmic_flops([10], [0, 4], 1, 1, 1, sliding_window=8),
                         4 * (7 + 8 + 8 + 8))

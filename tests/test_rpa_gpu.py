@@ -305,3 +305,19 @@ def test_decode_repeated_calls(gpu_device):
         assert bytes_equal(cache.cpu(), exp_cache)
     # A different batch on the same workspace afterwards.
     check(W.make_workload(DECODE_EDGE, 32, 8, 128, 16, seed=37, name="decode-after"), gpu_device)
+
+
+def test_decode_only_measurement_path(gpu_device):
+    """RPA_PATH_DECODE_ONLY launches the decode kernel alone: single-unit
+    decode rows are final; shapes the decode kernel does not take are rejected."""
+    # kv_len <= 32 keys: one 32-key tile, so every sequence is a single unit.
+    w = W.make_workload([(1, 20), (1, 7), (1, 32)], 8, 2, 128, 16, seed=38, name="dec-only")
+    exp_out, _ = O.ref_ragged_paged_attention(*w.args(), mode="fp32", skip_kv_update=True,
+                                              **w.kwargs)
+    out, _ = run_gpu(w, gpu_device, path=N.RPA_PATH_DECODE_ONLY, skip_kv_update=True)
+    assert_close(out, exp_out, 2e-2, 2e-2, "decode-only path, single-unit rows")
+    # Shapes the decode kernel does not take (f32 KV) are rejected.
+    p = W.make_workload([(1, 40)], 8, 2, 128, 16, seed=39, q_dtype=torch.float32,
+                        kv_dtype=torch.float32, name="f32")
+    with pytest.raises(NotImplementedError):
+        run_gpu(p, gpu_device, path=N.RPA_PATH_DECODE_ONLY)

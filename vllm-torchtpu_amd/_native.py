@@ -34,6 +34,7 @@ RPA_ERR_ABI = -6
 
 RPA_PATH_AUTO = 0
 RPA_PATH_GENERIC = 1
+RPA_PATH_DECODE_ONLY = 2  # measurement: the decode kernel alone
 
 _TORCH_TO_RPA = {
     torch.float32: RPA_DTYPE_F32,

@@ -128,6 +128,7 @@ int rpa_validate_desc(const rpa_desc* d) {
   if (d->max_num_seqs <= 0 || d->pages_per_seq < 0) return RPA_ERR_INVALID_ARG;
   if (d->has_soft_cap && d->soft_cap == 0.0f) return RPA_ERR_INVALID_ARG;
   if (d->sliding_window < 0) return RPA_ERR_INVALID_ARG;
+  if (d->path < RPA_PATH_AUTO || d->path > RPA_PATH_DECODE_ONLY) return RPA_ERR_INVALID_ARG;
   // Implemented combinations.
   if (d->kv_dtype == RPA_DTYPE_F16 || d->q_dtype == RPA_DTYPE_F16) return RPA_ERR_UNSUPPORTED;
   if (d->out_dtype != RPA_DTYPE_F32 && d->out_dtype != RPA_DTYPE_BF16) return RPA_ERR_UNSUPPORTED;
@@ -178,6 +179,8 @@ int rpa_forward(const rpa_desc* d, const void* queries, const void* keys, const 
   if (align & 15u) return RPA_ERR_INVALID_ARG;
   hipStream_t s = static_cast<hipStream_t>(stream);
   rpa::Params p = make_params(d);
+  const bool decode_only = d->path == RPA_PATH_DECODE_ONLY;
+  if (decode_only && !use_decode_kernel(d, p)) return RPA_ERR_UNSUPPORTED;
   if (!use_fused_path(d, p)) {
     if (!d->skip_kv_update) {
       hipError_t e = rpa::launch_kv_update(p, dtype_bytes(d->kv_dtype), keys, values, kv_cache,
@@ -198,6 +201,7 @@ int rpa_forward(const rpa_desc* d, const void* queries, const void* keys, const 
                                       kv_cache, kv_lens, page_indices, cu_q_lens, distribution,
                                       out, s);
     if (e != hipSuccess) return RPA_ERR_LAUNCH;
+    if (decode_only) return RPA_OK;
   }
   hipError_t e = rpa::launch_finish(p, d->kv_dtype, d->out_dtype, ws, queries, keys, values,
                                     kv_cache, kv_lens, page_indices, cu_q_lens, distribution, out,

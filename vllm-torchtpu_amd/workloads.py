@@ -183,3 +183,77 @@ def baseline_config(idx: int, seed: int | None = None) -> Workload:
                              distribution=[16, 16, 32], sliding_window=4096, soft_cap=50.0,
                              name="C5")
     raise ValueError(idx)
+
+
+# ---------------------------------------------------------------------------
+# Algorithmic work of a call (what the benchmark's roofline divides by time).
+# ---------------------------------------------------------------------------
+def _attended_keys(kv_len, q_len, sliding_window):
+    """Keys a sequence's rows read from HBM at least once: R_s."""
+    if sliding_window is None:
+        return kv_len
+    return min(kv_len, q_len + sliding_window - 1)
+
+
+def algorithmic_bytes(kv_lens, cu_q_lens, num_seqs, hq, hkv, d, dp, page_size,
+                      q_bytes, kv_bytes, out_bytes, sliding_window=None, kv_write=True):
+    """Algorithmic HBM bytes of one RPA call: KV read of R_s tokens per
+    sequence (the new tokens, read from the k/v inputs, included once), the
+    new-KV write into pages (unless kv_write is False, i.e. skip_kv_update),
+    Q read, O write, page-table and metadata reads."""
+    total = 0
+    rec = 2 * hkv * dp * kv_bytes
+    for s in range(num_seqs):
+        q_len = int(cu_q_lens[s + 1]) - int(cu_q_lens[s])
+        kv_len = int(kv_lens[s])
+        total += _attended_keys(kv_len, q_len, sliding_window) * rec
+        if kv_write:
+            total += q_len * rec
+        total += q_len * hq * d * (q_bytes + out_bytes)
+        total += cdiv(kv_len, page_size) * 4
+    total += (3 * num_seqs + 4) * 4
+    return total
+
+
+def decode_kernel_bytes(kv_lens, cu_q_lens, num_seqs, hq, hkv, d, dp, page_size, q_bytes,
+                        kv_bytes, sliding_window=None):
+    """Algorithmic HBM bytes of the decode kernel alone, attention only
+    (skip_kv_update): the KV records of every decode sequence's key range,
+    its q row and its page-table entries, plus the metadata.  Output rows are
+    not counted (multi-unit sequences write theirs in the finish kernel)."""
+    total = 0
+    rec = 2 * hkv * dp * kv_bytes
+    for s in range(num_seqs):
+        q_len = int(cu_q_lens[s + 1]) - int(cu_q_lens[s])
+        kv_len = int(kv_lens[s])
+        if q_len != 1 or kv_len < 1:
+            continue
+        total += _attended_keys(kv_len, 1, sliding_window) * rec
+        total += hq * d * q_bytes
+        total += cdiv(kv_len, page_size) * 4
+    total += (3 * num_seqs + 4) * 4
+    return total
+
+
+def algorithmic_flops(kv_lens, cu_q_lens, num_seqs, hq, d, sliding_window=None):
+    """4 * D * Hq * (sum over q rows of attended keys): QK^T and PV."""
+    tot = 0
+    for s in range(num_seqs):
+        q_len = int(cu_q_lens[s + 1]) - int(cu_q_lens[s])
+        kv_len = int(kv_lens[s])
+        for i in range(q_len):
+            a = kv_len - q_len + i + 1
+            if sliding_window is not None:
+                a = min(a, sliding_window)
+            tot += a
+    return 4 * d * hq * tot
+
+
+def prefill_flops(kv_lens, cu_q_lens, num_seqs, hq, d, sliding_window=None):
+    """algorithmic_flops over the rows of sequences with q_len > 1."""
+    tot = 0
+    for s in range(num_seqs):
+        q_len = int(cu_q_lens[s + 1]) - int(cu_q_lens[s])
+        if q_len > 1:
+            tot += algorithmic_flops([kv_lens[s]], [0, q_len], 1, hq, d, sliding_window)
+    return tot
