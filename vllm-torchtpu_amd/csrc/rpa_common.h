@@ -61,6 +61,25 @@ __device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
   return static_cast<uint16_t>(u >> 16);
 }
 
+// Four packed OCP fp8 values (byte i = element i) -> four bf16 values
+// (element i in bits [16i, 16i + 16) of the pair).  gfx950's
+// v_cvt_scalef32_pk_bf16_{fp8,bf8} with scale 1.0 converts two elements per
+// instruction; every e4m3fn / e5m2 value, subnormals included, is exactly
+// representable in bf16, so the result is exact (NaN stays NaN).
+template <bool kE5M2>
+__device__ __forceinline__ uint2 fp8x4_to_bf16x4(uint32_t w) {
+  typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+  bf16x2_t lo, hi;
+  if constexpr (kE5M2) {
+    lo = __builtin_amdgcn_cvt_scalef32_pk_bf16_bf8(static_cast<int>(w), 1.0f, false);
+    hi = __builtin_amdgcn_cvt_scalef32_pk_bf16_bf8(static_cast<int>(w), 1.0f, true);
+  } else {
+    lo = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(static_cast<int>(w), 1.0f, false);
+    hi = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(static_cast<int>(w), 1.0f, true);
+  }
+  return make_uint2(__builtin_bit_cast(uint32_t, lo), __builtin_bit_cast(uint32_t, hi));
+}
+
 // OCP fp8 e4m3fn: 1 sign, 4 exponent (bias 7), 3 mantissa; S.1111.111 = NaN,
 // no infinities; subnormals are m * 2^-9.
 __device__ __forceinline__ float fp8e4m3_to_f32(uint8_t x) {

@@ -67,27 +67,6 @@ struct KvBF16 {
   static __device__ __forceinline__ uint4 to_bf16(raw_t r) { return r; }
 };
 
-// fp8 -> bf16 bits, exact (every e4m3/e5m2 value is representable in bf16).
-__device__ __forceinline__ uint32_t e4m3_to_bf16_bits(uint32_t x) {
-  const uint32_t sign = (x & 0x80u) << 8;
-  const uint32_t mag = x & 0x7fu;
-  uint32_t r;
-  if (mag == 0x7fu) {
-    r = 0x7fc0u;  // NaN
-  } else if (mag >= 8u) {
-    r = (mag << 4) + (120u << 7);  // normal: exponent rebias 7 -> 127
-  } else {
-    // subnormal m * 2^-9: exact through f32
-    r = __float_as_uint(static_cast<float>(mag) * 0x1p-9f) >> 16;
-  }
-  return sign | r;
-}
-__device__ __forceinline__ uint32_t e5m2_to_bf16_bits(uint32_t x) {
-  const float f = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(x << 8)));
-  const uint32_t u = __float_as_uint(f);
-  return ((u & 0x7fffffffu) > 0x7f800000u) ? ((u >> 16) | 0x40u) : (u >> 16);
-}
-
 template <bool kE5M2>
 struct KvFP8 {
   static constexpr bool kIsE5M2 = kE5M2;
@@ -97,18 +76,9 @@ struct KvFP8 {
   static __device__ __forceinline__ raw_t load8(const storage* p) {
     return *reinterpret_cast<const uint2*>(p);
   }
-  static __device__ __forceinline__ uint32_t cvt(uint32_t b) {
-    return kE5M2 ? e5m2_to_bf16_bits(b) : e4m3_to_bf16_bits(b);
-  }
   static __device__ __forceinline__ uint4 to_bf16(raw_t raw) {
-    uint32_t w[8];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      w[i] = cvt((raw.x >> (8 * i)) & 0xffu);
-      w[4 + i] = cvt((raw.y >> (8 * i)) & 0xffu);
-    }
-    return make_uint4(w[0] | (w[1] << 16), w[2] | (w[3] << 16), w[4] | (w[5] << 16),
-                      w[6] | (w[7] << 16));
+    const uint2 a = fp8x4_to_bf16x4<kE5M2>(raw.x), b = fp8x4_to_bf16x4<kE5M2>(raw.y);
+    return make_uint4(a.x, a.y, b.x, b.y);
   }
 };
 
@@ -120,14 +90,6 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
 }
 
 
-// Raw 16-byte piece -> bf16 elements (8 for bf16, 16 for fp8 = two uint4).
-__device__ __forceinline__ uint32_t cvt_pair_e4m3(uint32_t b2) {
-  return e4m3_to_bf16_bits(b2 & 0xffu) | (e4m3_to_bf16_bits((b2 >> 8) & 0xffu) << 16);
-}
-__device__ __forceinline__ uint32_t cvt_pair_e5m2(uint32_t b2) {
-  return e5m2_to_bf16_bits(b2 & 0xffu) | (e5m2_to_bf16_bits((b2 >> 8) & 0xffu) << 16);
-}
-
 // Store one 16-byte load piece (raw KV bytes) as bf16 into an LDS row at
 // element offset e0.
 template <typename KV>
@@ -135,16 +97,10 @@ __device__ __forceinline__ void store_piece_bf16(unsigned char* row, int e0, uin
   if constexpr (sizeof(typename KV::storage) == 2) {
     *reinterpret_cast<uint4*>(row + 2 * e0) = raw;
   } else {
-    constexpr bool e5 = KV::kIsE5M2;
-    const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
-    uint32_t o[8];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      o[2 * i] = e5 ? cvt_pair_e5m2(w[i] & 0xffffu) : cvt_pair_e4m3(w[i] & 0xffffu);
-      o[2 * i + 1] = e5 ? cvt_pair_e5m2(w[i] >> 16) : cvt_pair_e4m3(w[i] >> 16);
-    }
-    *reinterpret_cast<uint4*>(row + 2 * e0) = make_uint4(o[0], o[1], o[2], o[3]);
-    *reinterpret_cast<uint4*>(row + 2 * e0 + 16) = make_uint4(o[4], o[5], o[6], o[7]);
+    const uint4 a = KV::to_bf16(make_uint2(raw.x, raw.y));
+    const uint4 b = KV::to_bf16(make_uint2(raw.z, raw.w));
+    *reinterpret_cast<uint4*>(row + 2 * e0) = a;
+    *reinterpret_cast<uint4*>(row + 2 * e0 + 16) = b;
   }
 }
 
