@@ -35,6 +35,7 @@ struct Params {
   int32_t ps_shift;        // log2(ps) when ps is a power of two, else -1
   int32_t skip_kv_update;  // new tokens are already in the cache (read them from there)
   int32_t decode_waves;    // wavefronts of the decode kernel's persistent grid (0: no decode kernel)
+  int32_t prefill_on;      // the prefill kernel attends the non-decode rows
 };
 
 // Page and slot of logical position j (>= 0): shifts for power-of-two page

@@ -12,7 +12,8 @@
 //           its cache page (kernel.py:154-166), unless skip_kv_update.
 //   attend  (token row t, q head g) of a non-decode sequence: generic_row
 //           attention, reading this call's new tokens from the k/v inputs
-//           (the write items of the same launch may not have run yet).
+//           (the write items of the same launch may not have run yet); only
+//           when the prefill kernel (rpa_prefill.hip) did not run.
 // Every workgroup first derives the decode kernel's plan (rpa_plan.h) from
 // the device-resident metadata.
 #include "rpa_common.h"
@@ -57,7 +58,8 @@ finish_kernel(Params p, const uint16_t* __restrict__ q, const typename KVT::stor
   }
   const int32_t nmerge = decode_on ? n * p.Hkv : 0;
   const int32_t nwrite = p.skip_kv_update ? 0 : p.T;
-  const int64_t total = static_cast<int64_t>(nmerge) + nwrite + static_cast<int64_t>(p.T) * p.Hq;
+  const int64_t nattend = p.prefill_on ? 0 : static_cast<int64_t>(p.T) * p.Hq;
+  const int64_t total = static_cast<int64_t>(nmerge) + nwrite + nattend;
   const int32_t rows = min(p.qpk, 16);
   const int32_t rp = decode_slot_rows(p.qpk);
   const int32_t kv_cap = p.pps * p.ps;

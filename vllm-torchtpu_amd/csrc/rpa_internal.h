@@ -64,9 +64,18 @@ hipError_t launch_decode(const Params& p, int kv_dtype, int out_dtype, const Dec
                          const int32_t* kv_lens, const int32_t* page_indices, const int32_t* cu,
                          const int32_t* dist, void* out, hipStream_t stream);
 
-// Finish kernel: merges the decode partials, and runs every other row
-// (attention plus its new tokens' cache write).  With p.decode_waves == 0 it
-// handles every row.
+// Prefill kernel: MFMA attention of every row the decode kernel does not
+// take (new tokens read from k/v; their cache write is the finish kernel's).
+bool prefill_supported(const Params& p, int q_dtype, int kv_dtype, int out_dtype);
+hipError_t launch_prefill(const Params& p, int kv_dtype, int out_dtype, const void* q,
+                          const void* k, const void* v, const void* cache,
+                          const int32_t* kv_lens, const int32_t* page_indices,
+                          const int32_t* cu, const int32_t* dist, void* out,
+                          hipStream_t stream);
+
+// Finish kernel: merges the decode partials, writes the new tokens of every
+// non-decode row into the cache and, unless p.prefill_on, attends those rows
+// too.  With p.decode_waves == 0 every row is a non-decode row.
 bool finish_supported(const Params& p, int q_dtype, int kv_dtype, int out_dtype);
 int finish_blocks(const Params& p, int num_cus);
 hipError_t launch_finish(const Params& p, int kv_dtype, int out_dtype, const DecodeWorkspace& ws,

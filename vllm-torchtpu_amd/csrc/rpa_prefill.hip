@@ -1,0 +1,425 @@
+// Prefill attention (rows of sequences with several query tokens) for gfx950.
+//
+// MFMA flash attention over the paged cache.  A workgroup (4 wavefronts)
+// owns one item: 128 q rows of one sequence and one kv head -- BQ = 128 / qpk
+// consecutive query tokens times the qpk q heads that share the kv head (GQA
+// packing: the K/V tiles of the kv head are read once for all of them).
+// Wavefront w owns rows [32w, 32w + 32).  Keys are streamed in 32-key tiles,
+// staged through double-buffered LDS as bf16 (fp8 KV converted on the way),
+// the next tile's global loads in flight in registers while the current one
+// is consumed.
+//
+// Per tile a wavefront computes, with v_mfma_f32_32x32x16_bf16,
+//   S^T[key, row] = K[key, :] . Q^T[:, row]          (A = K from LDS, B = Q^T in registers)
+//   O^T[dim, row] += V^T[dim, key] . P^T[key, row]    (A = V^T via ds_read_b64_tr_b16, B = P^T)
+// Lane l owns MFMA column l % 32 -- one q row -- in every accumulator, so the
+// online softmax needs one cross-lane exchange (lanes l and l ^ 32) per tile
+// and P feeds the PV product straight from the S^T accumulator registers.
+// The accumulator holds, for lane half c = l / 32, keys 8(i / 4) + 4c + i % 4
+// (register i); the PV k-step built from registers 0..7 therefore covers keys
+// {0-3, 8-11} (c = 0) and {4-7, 12-15} (c = 1), and the V^T operand is read
+// with the same key permutation (two 4-key transposing reads per k-step).
+//
+// Semantics (ref_ragged_paged_attention, kernel.py:185-209): row i of
+// sequence s sits at position p = kv_len - q_len + i; keys j <= p (and
+// j > p - W under a window) with s_j = q . k_j * sm_scale * k_scale * q_scale,
+// optional soft cap, softmax, out = P . V * v_scale.  New tokens (positions
+// >= kv_len - q_len) are read from the k/v inputs unless skip_kv_update, as
+// the Pallas kernel does (kernel.py:634-641); the finish kernel, launched
+// after this one, writes them into their pages.  P is rounded to bf16 for
+// the PV product (kernel.py:553); everything else accumulates in fp32.
+#include "rpa_common.h"
+#include "rpa_internal.h"
+#include "rpa_plan.h"
+
+namespace rpa {
+
+namespace {
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+typedef short v4i16 __attribute__((ext_vector_type(4)));
+
+constexpr int kThreads = 256;
+constexpr int kRows = 128;  // q rows per item (32 per wavefront)
+constexpr int BK = 32;      // keys per tile
+constexpr float kLog2e = 1.4426950408889634f;
+
+// KV element types: 8 elements per load piece, converted to 8 bf16.
+struct PKvBF16 {
+  using storage = uint16_t;
+  static __device__ __forceinline__ uint4 load8(const storage* p) {
+    return *reinterpret_cast<const uint4*>(p);
+  }
+};
+template <bool kE5M2>
+struct PKvFP8 {
+  using storage = uint8_t;
+  static __device__ __forceinline__ uint4 load8(const storage* p) {
+    const uint2 r = *reinterpret_cast<const uint2*>(p);
+    const uint2 a = fp8x4_to_bf16x4<kE5M2>(r.x), b = fp8x4_to_bf16x4<kE5M2>(r.y);
+    return make_uint4(a.x, a.y, b.x, b.y);
+  }
+};
+
+// Round-to-nearest-even pair of f32 -> packed bf16 (the hardware conversion).
+__device__ __forceinline__ uint32_t pack_bf16x2_rne(float lo, float hi) {
+  typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+  typedef float f32x2_t __attribute__((ext_vector_type(2)));
+  const bf16x2_t r = __builtin_convertvector(f32x2_t{lo, hi}, bf16x2_t);
+  return __builtin_bit_cast(uint32_t, r);
+}
+
+template <int DP>
+struct PrefillCfg {
+  static constexpr int KS = 2 * DP + 16;         // LDS K row stride (bytes)
+  static constexpr int VS = 2 * DP + 32;         // LDS V row stride (bytes)
+  static constexpr int BUF = BK * (KS + VS);     // one K|V tile buffer
+  static constexpr int PIECES = BK * 2 * DP / 8;  // 8-element pieces per tile
+  static constexpr int PPT = PIECES / kThreads;   // pieces per thread
+  static constexpr int KSTEPS = DP / 16;          // QK^T k-steps over head_dim
+  static constexpr int NT = DP / 32;              // 32-dim output blocks
+  static_assert(PIECES % kThreads == 0, "whole pieces per thread");
+};
+
+// Which sequences this kernel owns: every sequence with rows, except the
+// decode sequences when the decode kernel runs.
+__device__ __forceinline__ int32_t prefill_blocks(const Params& p, const int32_t* cu,
+                                                  const int32_t* kv_lens, int32_t s, int32_t bq,
+                                                  bool decode_on) {
+  int32_t kl;
+  if (decode_on && is_decode_seq(p, cu, kv_lens, s, &kl)) return 0;
+  const int32_t q_len = cu[s + 1] - cu[s];
+  if (q_len <= 0) return 0;
+  return (q_len + bq - 1) / bq;
+}
+
+// Two workgroups per CU at head_dim 128 (256 registers per lane), one at 256.
+template <typename KV, int DP, typename OutS>
+__global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(DP == 128 ? 2 : 1)))
+prefill_kernel(Params p, const uint16_t* __restrict__ q,
+               const typename KV::storage* __restrict__ keys,
+               const typename KV::storage* __restrict__ values,
+               const typename KV::storage* __restrict__ cache,
+               const int32_t* __restrict__ kv_lens, const int32_t* __restrict__ page_indices,
+               const int32_t* __restrict__ cu, const int32_t* __restrict__ dist,
+               OutS* __restrict__ out) {
+  using C = PrefillCfg<DP>;
+  using E = typename KV::storage;
+  __shared__ __align__(16) unsigned char smem[2 * C::BUF];
+  __shared__ int32_t blk[kMaxDecodeSeqs + 1];
+  __shared__ int32_t red[3 * kPlanWaves];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int col = lane & 31;  // MFMA column: this lane's q row within the wavefront
+  const int half = lane >> 5;
+  const bool decode_on = p.decode_waves > 0;
+  const int32_t bq = kRows / p.qpk;  // query tokens per item
+
+  // ---- item: (block kb over all owned sequences, kv head h) --------------
+  const int32_t n = min(num_seqs_of(dist, p.S), kMaxDecodeSeqs);
+  for (int32_t s = tid; s < n; s += kThreads)
+    blk[s] = prefill_blocks(p, cu, kv_lens, s, bq, decode_on);
+  __syncthreads();
+  block_exclusive_scan(blk, n, red);
+  const int32_t total = blk[n];
+  const int32_t h = static_cast<int32_t>(blockIdx.x % p.Hkv);
+  // Later blocks of a sequence attend to more keys: walk blocks from the
+  // last one so the longest items start first.
+  const int32_t kb_rev = static_cast<int32_t>(blockIdx.x / p.Hkv);
+  if (kb_rev >= total) return;
+  const int32_t kb = total - 1 - kb_rev;
+  const int32_t s = find_prefix(blk, n, kb);
+  const int32_t b = kb - blk[s];
+  const int32_t q_start = cu[s];
+  const int32_t q_len = cu[s + 1] - q_start;
+  // Rows outside [0, T) are never read or written (metadata out of contract).
+  if (q_start < 0 || q_len <= 0 || q_start + q_len > p.T) return;
+  const int32_t kv_cap = p.pps * p.ps;
+  const int32_t kv_len = min(kv_lens[s], kv_cap);
+  const int32_t new_start = kv_len - q_len;
+  const bool new_from_input = p.skip_kv_update == 0;
+  const int32_t* ptab = page_indices + static_cast<int64_t>(s) * p.pps;
+
+  // Rows of this item: row r -> query token i = b * bq + r / qpk, q head
+  // h * qpk + r % qpk; valid when r < bq * qpk and i < q_len.
+  const int32_t tok0 = b * bq;
+  const int32_t ntok = min(bq, q_len - tok0);
+  const int32_t pos_first = new_start + tok0;
+  const int32_t pos_last = new_start + tok0 + ntok - 1;
+  // Key range of the whole item.
+  int32_t lo = 0, hi = kv_len;
+  if (p.causal) {
+    hi = min(kv_len, pos_last + 1);
+    if (p.window > 0) lo = max(0, pos_first - p.window + 1);
+  }
+  const int32_t ntiles = hi > lo ? (hi - lo + BK - 1) / BK : 0;
+
+  // This lane's row.
+  const int32_t r = wave * 32 + col;
+  const int32_t ti = r / p.qpk;
+  const bool row_ok = ti < ntok && r < bq * p.qpk;
+  const int32_t tok = tok0 + min(ti, ntok - 1);
+  const int32_t qhead = h * p.qpk + r % p.qpk;
+  const int32_t pos = new_start + tok;
+  int32_t row_lo = 0, row_hi = kv_len;  // keys this row attends: [row_lo, row_hi)
+  if (p.causal) {
+    row_hi = min(kv_len, pos + 1);
+    if (p.window > 0) row_lo = max(0, pos - p.window + 1);
+  }
+  // The wavefront's key range (for skipping tiles no row of it attends).
+  const int32_t wr_first = min(wave * 32, bq * p.qpk - 1) / p.qpk;
+  const int32_t wr_last = min(wave * 32 + 31, bq * p.qpk - 1) / p.qpk;
+  int32_t w_lo = 0, w_hi = kv_len;
+  if (p.causal) {
+    w_hi = min(kv_len, new_start + tok0 + min(wr_last, ntok - 1) + 1);
+    if (p.window > 0) w_lo = max(0, new_start + tok0 + min(wr_first, ntok - 1) - p.window + 1);
+  }
+  const bool wave_live = wave * 32 < bq * p.qpk && tok0 + wr_first < q_len;
+
+  // ---- Q^T operand (B of S^T): column = row, k-slots 8 * half .. + 7 of
+  // each 16-dim k-step.
+  uint4 qop[C::KSTEPS];
+  {
+    const uint16_t* qrow = q + (static_cast<int64_t>(q_start + tok) * p.Hq + qhead) * p.D;
+#pragma unroll
+    for (int kk = 0; kk < C::KSTEPS; ++kk) {
+      const int d0 = 16 * kk + 8 * half;
+      qop[kk] = d0 < p.D ? *reinterpret_cast<const uint4*>(qrow + d0) : make_uint4(0u, 0u, 0u, 0u);
+    }
+  }
+
+  // ---- tile staging: piece c of key `key` (c < Dp / 8: K, else V) ------------
+  uint4 stage[C::PPT];
+  auto load_tile = [&](int32_t t) __attribute__((always_inline)) {
+    const int32_t k0 = lo + t * BK;
+#pragma unroll
+    for (int i = 0; i < C::PPT; ++i) {
+      const int idx = tid + i * kThreads;
+      const int key = idx / (2 * DP / 8);
+      const int c = idx % (2 * DP / 8);
+      const int isv = c >= DP / 8;
+      const int e0 = (c - isv * (DP / 8)) * 8;
+      const int32_t j = min(k0 + key, hi - 1);  // keys past the range: copies of a valid key
+      uint4 v = make_uint4(0u, 0u, 0u, 0u);
+      if (e0 < p.D) {
+        const E* src;
+        if (new_from_input && j >= new_start) {
+          const int64_t row = min(q_start + (j - new_start), p.T - 1);
+          src = (isv ? values : keys) + (row * p.Hkv + h) * p.D + e0;
+        } else {
+          const int32_t pg = min(max(ptab[page_of(p, j)], 0), p.P - 1);
+          src = cache + (static_cast<int64_t>(pg) * p.ps + slot_of(p, j)) * p.rec +
+                static_cast<int64_t>(2 * h + isv) * DP + e0;
+        }
+        v = KV::load8(src);
+      }
+      stage[i] = v;
+    }
+  };
+  auto store_tile = [&](unsigned char* buf) __attribute__((always_inline)) {
+    unsigned char* kb_ = buf;
+    unsigned char* vb_ = buf + BK * C::KS;
+#pragma unroll
+    for (int i = 0; i < C::PPT; ++i) {
+      const int idx = tid + i * kThreads;
+      const int key = idx / (2 * DP / 8);
+      const int c = idx % (2 * DP / 8);
+      const int isv = c >= DP / 8;
+      const int e0 = (c - isv * (DP / 8)) * 8;
+      unsigned char* dst = isv ? vb_ + key * C::VS + 2 * e0 : kb_ + key * C::KS + 2 * e0;
+      *reinterpret_cast<uint4*>(dst) = stage[i];
+    }
+  };
+
+  f32x16_t oacc[C::NT];
+#pragma unroll
+  for (int t = 0; t < C::NT; ++t) oacc[t] = f32x16_t{};
+  float m_run = -INFINITY;  // log2 units
+  float l_run = 0.0f;       // this lane's share of the row sum
+
+  if (ntiles > 0) {
+    load_tile(0);
+    store_tile(smem);
+  }
+  __syncthreads();
+  for (int32_t t = 0; t < ntiles; ++t) {
+    if (t + 1 < ntiles) load_tile(t + 1);
+    const unsigned char* kbuf = smem + (t & 1) * C::BUF;
+    const unsigned char* vbuf = kbuf + BK * C::KS;
+    const int32_t k0 = lo + t * BK;
+    // Tiles outside the wavefront's key range are skipped (wave-uniform).
+    if (wave_live && k0 < w_hi && k0 + BK > w_lo) {
+      // S^T = K . Q^T: A lane l -> key l % 32, dims 16kk + 8 half .. + 7.
+      f32x16_t sacc = f32x16_t{};
+#pragma unroll
+      for (int kk = 0; kk < C::KSTEPS; ++kk) {
+        const uint4 kv = *reinterpret_cast<const uint4*>(kbuf + col * C::KS + 2 * (16 * kk + 8 * half));
+        sacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, kv),
+                                                       __builtin_bit_cast(bf16x8_t, qop[kk]),
+                                                       sacc, 0, 0, 0);
+      }
+      // Scores of this lane's row: register i -> key k0 + 8(i/4) + 4 half + i%4.
+      float sc[16];
+      float tmax = -INFINITY;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        float x = sacc[i] * p.score_scale;
+        if (p.has_cap) x = soft_cap_fn(x, p.cap, p.inv_cap);
+        x *= kLog2e;
+        const int32_t j = k0 + 8 * (i >> 2) + 4 * half + (i & 3);
+        x = (j >= row_lo && j < row_hi) ? x : -INFINITY;
+        sc[i] = x;
+        tmax = fmaxf(tmax, x);
+      }
+      tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+      const float m_new = fmaxf(m_run, tmax);
+      // Rows with no valid key yet keep m = -inf and contribute nothing.
+      const float m_use = (m_new == -INFINITY) ? 0.0f : m_new;
+      const float alpha = (m_run == -INFINITY) ? 0.0f : exp2f(m_run - m_use);
+      float psum = 0.0f;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        sc[i] = exp2f(sc[i] - m_use);  // exp2(-inf) = 0 for masked keys
+        psum += sc[i];
+      }
+      l_run = l_run * alpha + psum;
+      m_run = m_new;
+      // Rescale the output only when some row's max moved (wave-uniform test).
+      if (__any(alpha != 1.0f)) {
+#pragma unroll
+        for (int tt = 0; tt < C::NT; ++tt) oacc[tt] *= alpha;
+      }
+      // P^T operands: k-step ks from registers 8ks .. 8ks + 7.
+      uint4 pop[2];
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks)
+        pop[ks] = make_uint4(pack_bf16x2_rne(sc[8 * ks + 0], sc[8 * ks + 1]),
+                             pack_bf16x2_rne(sc[8 * ks + 2], sc[8 * ks + 3]),
+                             pack_bf16x2_rne(sc[8 * ks + 4], sc[8 * ks + 5]),
+                             pack_bf16x2_rne(sc[8 * ks + 6], sc[8 * ks + 7]));
+      // O^T += V^T . P^T.  V^T operand lane l -> dim 32tt + l % 32; k-slots
+      // 0..3 -> keys 16ks + 4 half + 0..3, slots 4..7 -> keys 16ks + 8 + 4 half
+      // + 0..3.  ds_read_b64_tr_b16 in 16-lane group G: source lane j points at
+      // key kbase + j / 4, dims d0 + 4 (j % 4); lane n receives
+      // V[kbase + 0..3][d0 + n].
+      const int G = lane >> 4, jl = lane & 15;
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) {
+        const int key_a = 16 * ks + 4 * (G >> 1) + (jl >> 2);
+        const unsigned char* ra = vbuf + key_a * C::VS + 2 * (16 * (G & 1) + 4 * (jl & 3));
+        const unsigned char* rb = ra + 8 * C::VS;
+#pragma unroll
+        for (int tt = 0; tt < C::NT; ++tt) {
+          const v4i16 va = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+              (__attribute__((address_space(3))) v4i16*)(ra + 64 * tt));
+          const v4i16 vb = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+              (__attribute__((address_space(3))) v4i16*)(rb + 64 * tt));
+          const uint2 ua = __builtin_bit_cast(uint2, va), ub = __builtin_bit_cast(uint2, vb);
+          const uint4 vop = make_uint4(ua.x, ua.y, ub.x, ub.y);
+          oacc[tt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, vop),
+                                                             __builtin_bit_cast(bf16x8_t, pop[ks]),
+                                                             oacc[tt], 0, 0, 0);
+        }
+      }
+    }
+    if (t + 1 < ntiles) store_tile(smem + ((t + 1) & 1) * C::BUF);
+    __syncthreads();
+  }
+
+  // ---- output: lane l, block tt, register i -> dim 32tt + 8(i/4) + 4 half + i%4.
+  const float lsum = l_run + __shfl_xor(l_run, 32, 64);
+  if (!row_ok) return;
+  const float inv = (lsum == 0.0f) ? 0.0f : p.v_scale / lsum;
+  OutS* orow = out + (static_cast<int64_t>(q_start + tok) * p.Hq + qhead) * p.D;
+#pragma unroll
+  for (int tt = 0; tt < C::NT; ++tt)
+#pragma unroll
+    for (int g4 = 0; g4 < 4; ++g4) {
+      const int d = 32 * tt + 8 * g4 + 4 * half;
+      if (d >= p.D) continue;
+      const float v0 = oacc[tt][4 * g4 + 0] * inv, v1 = oacc[tt][4 * g4 + 1] * inv;
+      const float v2 = oacc[tt][4 * g4 + 2] * inv, v3 = oacc[tt][4 * g4 + 3] * inv;
+      if constexpr (sizeof(OutS) == 4) {
+        *reinterpret_cast<float4*>(orow + d) = make_float4(v0, v1, v2, v3);
+      } else {
+        *reinterpret_cast<uint2*>(orow + d) =
+            make_uint2(static_cast<uint32_t>(f32_to_bf16_bits(v0)) |
+                           (static_cast<uint32_t>(f32_to_bf16_bits(v1)) << 16),
+                       static_cast<uint32_t>(f32_to_bf16_bits(v2)) |
+                           (static_cast<uint32_t>(f32_to_bf16_bits(v3)) << 16));
+      }
+    }
+}
+
+template <typename KV, typename OutS>
+hipError_t launch_dp(const Params& p, const void* q, const void* k, const void* v,
+                     const void* cache, const int32_t* kv_lens, const int32_t* page_indices,
+                     const int32_t* cu, const int32_t* dist, void* out, hipStream_t stream) {
+  using E = typename KV::storage;
+  // Upper bound on items: every sequence adds at most one partial block.
+  const int32_t bq = kRows / p.qpk;
+  const int64_t blocks = (static_cast<int64_t>(p.T) + bq - 1) / bq + p.S;
+  const int64_t grid = blocks * p.Hkv;
+  if (grid > 0x7fffffff) return hipErrorInvalidValue;
+  const dim3 g(static_cast<uint32_t>(grid)), blk(kThreads);
+#define RPA_PREFILL_LAUNCH(DPV)                                                              \
+  hipLaunchKernelGGL((prefill_kernel<KV, DPV, OutS>), g, blk, 0, stream, p,                 \
+                     static_cast<const uint16_t*>(q), static_cast<const E*>(k),             \
+                     static_cast<const E*>(v), static_cast<const E*>(cache), kv_lens,       \
+                     page_indices, cu, dist, static_cast<OutS*>(out))
+  if (p.Dp == 128) {
+    RPA_PREFILL_LAUNCH(128);
+  } else if (p.Dp == 256) {
+    RPA_PREFILL_LAUNCH(256);
+  } else {
+    return hipErrorInvalidValue;
+  }
+#undef RPA_PREFILL_LAUNCH
+  return hipGetLastError();
+}
+
+template <typename OutS>
+hipError_t launch_kv(const Params& p, int kv_dtype, const void* q, const void* k, const void* v,
+                     const void* cache, const int32_t* kv_lens, const int32_t* page_indices,
+                     const int32_t* cu, const int32_t* dist, void* out, hipStream_t stream) {
+  switch (kv_dtype) {
+    case RPA_DTYPE_BF16:
+      return launch_dp<PKvBF16, OutS>(p, q, k, v, cache, kv_lens, page_indices, cu, dist, out, stream);
+    case RPA_DTYPE_FP8_E4M3FN:
+      return launch_dp<PKvFP8<false>, OutS>(p, q, k, v, cache, kv_lens, page_indices, cu, dist, out, stream);
+    case RPA_DTYPE_FP8_E5M2:
+      return launch_dp<PKvFP8<true>, OutS>(p, q, k, v, cache, kv_lens, page_indices, cu, dist, out, stream);
+    default:
+      return hipErrorInvalidValue;
+  }
+}
+
+}  // namespace
+
+bool prefill_supported(const Params& p, int q_dtype, int kv_dtype, int out_dtype) {
+  if (q_dtype != RPA_DTYPE_BF16) return false;
+  if (kv_dtype != RPA_DTYPE_BF16 && kv_dtype != RPA_DTYPE_FP8_E4M3FN &&
+      kv_dtype != RPA_DTYPE_FP8_E5M2)
+    return false;
+  if (out_dtype != RPA_DTYPE_BF16 && out_dtype != RPA_DTYPE_F32) return false;
+  if (p.Dp != 128 && p.Dp != 256) return false;
+  // 8-element pieces of q / k / v rows; at least one query token per item.
+  if (p.D % 8 != 0 || p.qpk > kRows) return false;
+  if (p.S > kMaxDecodeSeqs) return false;
+  return true;
+}
+
+hipError_t launch_prefill(const Params& p, int kv_dtype, int out_dtype, const void* q,
+                          const void* k, const void* v, const void* cache,
+                          const int32_t* kv_lens, const int32_t* page_indices,
+                          const int32_t* cu, const int32_t* dist, void* out,
+                          hipStream_t stream) {
+  if (out_dtype == RPA_DTYPE_F32)
+    return launch_kv<float>(p, kv_dtype, q, k, v, cache, kv_lens, page_indices, cu, dist, out, stream);
+  return launch_kv<uint16_t>(p, kv_dtype, q, k, v, cache, kv_lens, page_indices, cu, dist, out, stream);
+}
+
+}  // namespace rpa
