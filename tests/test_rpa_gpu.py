@@ -321,3 +321,12 @@ def test_decode_only_measurement_path(gpu_device):
                         kv_dtype=torch.float32, name="f32")
     with pytest.raises(NotImplementedError):
         run_gpu(p, gpu_device, path=N.RPA_PATH_DECODE_ONLY)
+
+
+@pytest.mark.parametrize("scale", [0.0, -0.05])
+def test_non_positive_sm_scale(gpu_device, scale):
+    """sm_scale is a plain multiplier: zero gives uniform attention over the
+    visible keys, a negative one flips the ranking (decode and prefill rows)."""
+    check(W.make_workload([(1, 70), (9, 40), (33, 33)], 8, 2, 128, 16, seed=40,
+                          distribution=[1, 1, 3], name=f"scale{scale}", sm_scale=scale),
+          gpu_device)

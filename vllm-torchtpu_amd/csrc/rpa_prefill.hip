@@ -42,7 +42,6 @@ typedef short v4i16 __attribute__((ext_vector_type(4)));
 
 constexpr int kThreads = 256;
 constexpr int kRows = 128;  // q rows per item (32 per wavefront)
-constexpr int BK = 32;      // keys per tile
 constexpr float kLog2e = 1.4426950408889634f;
 
 // KV element types: 8 elements per load piece, converted to 8 bf16.
@@ -72,15 +71,26 @@ __device__ __forceinline__ uint32_t pack_bf16x2_rne(float lo, float hi) {
 
 template <int DP>
 struct PrefillCfg {
-  static constexpr int KS = 2 * DP + 16;         // LDS K row stride (bytes)
-  static constexpr int VS = 2 * DP + 32;         // LDS V row stride (bytes)
-  static constexpr int BUF = BK * (KS + VS);     // one K|V tile buffer
-  static constexpr int PIECES = BK * 2 * DP / 8;  // 8-element pieces per tile
-  static constexpr int PPT = PIECES / kThreads;   // pieces per thread
-  static constexpr int KSTEPS = DP / 16;          // QK^T k-steps over head_dim
-  static constexpr int NT = DP / 32;              // 32-dim output blocks
-  static_assert(PIECES % kThreads == 0, "whole pieces per thread");
+  static constexpr int BK = DP == 128 ? 64 : 32;   // keys per tile
+  static constexpr int NSB = BK / 32;              // 32-key S^T blocks per tile
+  static constexpr int KS = 2 * DP + 16;           // LDS K row stride (bytes)
+  static constexpr int VS = 2 * DP + 32;           // LDS V row stride (bytes)
+  static constexpr int BUF = BK * (KS + VS);       // one K|V tile buffer
+  static constexpr int PPK = 2 * DP / 8;           // 8-element pieces per key (K then V)
+  static constexpr int KPI = kThreads / PPK;       // keys covered per staging step
+  static constexpr int PPT = BK / KPI;             // pieces per thread per tile
+  static constexpr int KSTEPS = DP / 16;           // QK^T k-steps over head_dim
+  static constexpr int NT = DP / 32;               // 32-dim output blocks
+  static_assert(kThreads % PPK == 0 && BK % KPI == 0, "whole pieces per thread");
+  static_assert(2 * BUF >= 4 * (kMaxDecodeSeqs + 1), "plan scratch fits the tile buffers");
 };
+
+// Page ids of an item's key range kept in LDS (longer ranges read the page
+// table directly).
+constexpr int kItemPages = 1024;
+// Lazy rescaling: a row's reference max moves only when a tile's max exceeds
+// it by more than 2^kRescaleLog2 (P values then stay below 2^8).
+constexpr float kRescaleLog2 = 8.0f;
 
 // Which sequences this kernel owns: every sequence with rows, except the
 // decode sequences when the decode kernel runs.
@@ -106,8 +116,9 @@ prefill_kernel(Params p, const uint16_t* __restrict__ q,
                OutS* __restrict__ out) {
   using C = PrefillCfg<DP>;
   using E = typename KV::storage;
+  constexpr int BK = C::BK;
   __shared__ __align__(16) unsigned char smem[2 * C::BUF];
-  __shared__ int32_t blk[kMaxDecodeSeqs + 1];
+  __shared__ int32_t pages[kItemPages];
   __shared__ int32_t red[3 * kPlanWaves];
 
   const int tid = threadIdx.x;
@@ -118,7 +129,9 @@ prefill_kernel(Params p, const uint16_t* __restrict__ q,
   const bool decode_on = p.decode_waves > 0;
   const int32_t bq = kRows / p.qpk;  // query tokens per item
 
-  // ---- item: (block kb over all owned sequences, kv head h) --------------
+  // ---- item: (block kb over all owned sequences, kv head h).  The block
+  // prefix lives in the (not yet used) tile buffers.
+  int32_t* blk = reinterpret_cast<int32_t*>(smem);
   const int32_t n = min(num_seqs_of(dist, p.S), kMaxDecodeSeqs);
   for (int32_t s = tid; s < n; s += kThreads)
     blk[s] = prefill_blocks(p, cu, kv_lens, s, bq, decode_on);
@@ -147,37 +160,47 @@ prefill_kernel(Params p, const uint16_t* __restrict__ q,
   // h * qpk + r % qpk; valid when r < bq * qpk and i < q_len.
   const int32_t tok0 = b * bq;
   const int32_t ntok = min(bq, q_len - tok0);
-  const int32_t pos_first = new_start + tok0;
-  const int32_t pos_last = new_start + tok0 + ntok - 1;
   // Key range of the whole item.
   int32_t lo = 0, hi = kv_len;
   if (p.causal) {
-    hi = min(kv_len, pos_last + 1);
-    if (p.window > 0) lo = max(0, pos_first - p.window + 1);
+    hi = min(kv_len, new_start + tok0 + ntok);
+    if (p.window > 0) lo = max(0, new_start + tok0 - p.window + 1);
   }
   const int32_t ntiles = hi > lo ? (hi - lo + BK - 1) / BK : 0;
 
-  // This lane's row.
+  // This lane's row, and the range of keys it attends: [row_lo, row_hi).
   const int32_t r = wave * 32 + col;
   const int32_t ti = r / p.qpk;
   const bool row_ok = ti < ntok && r < bq * p.qpk;
   const int32_t tok = tok0 + min(ti, ntok - 1);
   const int32_t qhead = h * p.qpk + r % p.qpk;
-  const int32_t pos = new_start + tok;
-  int32_t row_lo = 0, row_hi = kv_len;  // keys this row attends: [row_lo, row_hi)
-  if (p.causal) {
-    row_hi = min(kv_len, pos + 1);
-    if (p.window > 0) row_lo = max(0, pos - p.window + 1);
-  }
-  // The wavefront's key range (for skipping tiles no row of it attends).
-  const int32_t wr_first = min(wave * 32, bq * p.qpk - 1) / p.qpk;
-  const int32_t wr_last = min(wave * 32 + 31, bq * p.qpk - 1) / p.qpk;
-  int32_t w_lo = 0, w_hi = kv_len;
-  if (p.causal) {
-    w_hi = min(kv_len, new_start + tok0 + min(wr_last, ntok - 1) + 1);
-    if (p.window > 0) w_lo = max(0, new_start + tok0 + min(wr_first, ntok - 1) - p.window + 1);
-  }
-  const bool wave_live = wave * 32 < bq * p.qpk && tok0 + wr_first < q_len;
+  auto key_range = [&](int32_t token, int32_t* klo, int32_t* khi) {
+    const int32_t pos = new_start + token;
+    *klo = 0;
+    *khi = kv_len;
+    if (p.causal) {
+      *khi = min(kv_len, pos + 1);
+      if (p.window > 0) *klo = max(0, pos - p.window + 1);
+    }
+  };
+  int32_t row_lo, row_hi;
+  key_range(tok, &row_lo, &row_hi);
+  // The wavefront's rows span tokens [wt0, wt1]: tiles outside the union of
+  // their ranges are skipped, tiles inside the intersection need no mask.
+  const bool wave_live = wave * 32 < bq * p.qpk && wave * 32 / p.qpk < ntok;
+  const int32_t wt0 = tok0 + min(wave * 32 / p.qpk, ntok - 1);
+  const int32_t wt1 = tok0 + min(min(wave * 32 + 31, bq * p.qpk - 1) / p.qpk, ntok - 1);
+  int32_t w_lo0, w_hi0, w_lo1, w_hi1;  // ranges of the first and last token
+  key_range(wt0, &w_lo0, &w_hi0);
+  key_range(wt1, &w_lo1, &w_hi1);
+
+  // ---- page ids of the item's keys into LDS.
+  const int32_t pg0 = hi > lo ? page_of(p, lo) : 0;
+  const int32_t npg = hi > lo ? page_of(p, hi - 1) - pg0 + 1 : 0;
+  const bool lds_pages = npg <= kItemPages;
+  if (lds_pages)
+    for (int32_t i = tid; i < npg; i += kThreads) pages[i] = min(max(ptab[pg0 + i], 0), p.P - 1);
+  __syncthreads();  // the plan scratch is dead; the page ids are visible
 
   // ---- Q^T operand (B of S^T): column = row, k-slots 8 * half .. + 7 of
   // each 16-dim k-step.
@@ -191,28 +214,31 @@ prefill_kernel(Params p, const uint16_t* __restrict__ q,
     }
   }
 
-  // ---- tile staging: piece c of key `key` (c < Dp / 8: K, else V) ------------
+  // ---- tile staging.  Thread tid always moves piece c = tid % PPK (K for
+  // c < Dp / 8, else V; elements e0 .. e0 + 7) of keys tid / PPK + KPI * i.
+  const int pc = tid % C::PPK;
+  const int pkey = tid / C::PPK;
+  const int isv = pc >= DP / 8;
+  const int e0 = (pc - isv * (DP / 8)) * 8;
+  const bool piece_live = e0 < p.D;
+  const E* in_base = (isv ? values : keys) + static_cast<int64_t>(h) * p.D + e0;
+  const int64_t cache_off = static_cast<int64_t>(2 * h + isv) * DP + e0;
   uint4 stage[C::PPT];
   auto load_tile = [&](int32_t t) __attribute__((always_inline)) {
     const int32_t k0 = lo + t * BK;
 #pragma unroll
     for (int i = 0; i < C::PPT; ++i) {
-      const int idx = tid + i * kThreads;
-      const int key = idx / (2 * DP / 8);
-      const int c = idx % (2 * DP / 8);
-      const int isv = c >= DP / 8;
-      const int e0 = (c - isv * (DP / 8)) * 8;
-      const int32_t j = min(k0 + key, hi - 1);  // keys past the range: copies of a valid key
+      const int32_t j = min(k0 + pkey + C::KPI * i, hi - 1);  // past the range: a valid key
       uint4 v = make_uint4(0u, 0u, 0u, 0u);
-      if (e0 < p.D) {
+      if (piece_live) {
         const E* src;
         if (new_from_input && j >= new_start) {
           const int64_t row = min(q_start + (j - new_start), p.T - 1);
-          src = (isv ? values : keys) + (row * p.Hkv + h) * p.D + e0;
+          src = in_base + row * p.Hkv * p.D;
         } else {
-          const int32_t pg = min(max(ptab[page_of(p, j)], 0), p.P - 1);
-          src = cache + (static_cast<int64_t>(pg) * p.ps + slot_of(p, j)) * p.rec +
-                static_cast<int64_t>(2 * h + isv) * DP + e0;
+          const int32_t pg = lds_pages ? pages[page_of(p, j) - pg0]
+                                       : min(max(ptab[page_of(p, j)], 0), p.P - 1);
+          src = cache + (static_cast<int64_t>(pg) * p.ps + slot_of(p, j)) * p.rec + cache_off;
         }
         v = KV::load8(src);
       }
@@ -220,25 +246,20 @@ prefill_kernel(Params p, const uint16_t* __restrict__ q,
     }
   };
   auto store_tile = [&](unsigned char* buf) __attribute__((always_inline)) {
-    unsigned char* kb_ = buf;
-    unsigned char* vb_ = buf + BK * C::KS;
+    unsigned char* dst0 = isv ? buf + BK * C::KS + pkey * C::VS + 2 * e0
+                              : buf + pkey * C::KS + 2 * e0;
+    const int rstride = isv ? C::VS : C::KS;
 #pragma unroll
-    for (int i = 0; i < C::PPT; ++i) {
-      const int idx = tid + i * kThreads;
-      const int key = idx / (2 * DP / 8);
-      const int c = idx % (2 * DP / 8);
-      const int isv = c >= DP / 8;
-      const int e0 = (c - isv * (DP / 8)) * 8;
-      unsigned char* dst = isv ? vb_ + key * C::VS + 2 * e0 : kb_ + key * C::KS + 2 * e0;
-      *reinterpret_cast<uint4*>(dst) = stage[i];
-    }
+    for (int i = 0; i < C::PPT; ++i)
+      *reinterpret_cast<uint4*>(dst0 + C::KPI * i * rstride) = stage[i];
   };
 
+  const float cm = p.has_cap ? 1.0f : p.score_scale * kLog2e;  // multiplier into log2 units
   f32x16_t oacc[C::NT];
 #pragma unroll
   for (int t = 0; t < C::NT; ++t) oacc[t] = f32x16_t{};
-  float m_run = -INFINITY;  // log2 units
-  float l_run = 0.0f;       // this lane's share of the row sum
+  float m_ref = -INFINITY;  // reference max of the row (log2 units)
+  float l_run = 0.0f;       // this lane's share of the row sum (relative to m_ref)
 
   if (ntiles > 0) {
     load_tile(0);
@@ -250,80 +271,102 @@ prefill_kernel(Params p, const uint16_t* __restrict__ q,
     const unsigned char* kbuf = smem + (t & 1) * C::BUF;
     const unsigned char* vbuf = kbuf + BK * C::KS;
     const int32_t k0 = lo + t * BK;
-    // Tiles outside the wavefront's key range are skipped (wave-uniform).
-    if (wave_live && k0 < w_hi && k0 + BK > w_lo) {
-      // S^T = K . Q^T: A lane l -> key l % 32, dims 16kk + 8 half .. + 7.
-      f32x16_t sacc = f32x16_t{};
+    if (wave_live && k0 < w_hi1 && k0 + BK > w_lo0) {
+      // S^T = K . Q^T per 32-key block: A lane l -> key l % 32, dims 16kk + 8 half ..
+      f32x16_t sacc[C::NSB];
+#pragma unroll
+      for (int sb = 0; sb < C::NSB; ++sb) sacc[sb] = f32x16_t{};
 #pragma unroll
       for (int kk = 0; kk < C::KSTEPS; ++kk) {
-        const uint4 kv = *reinterpret_cast<const uint4*>(kbuf + col * C::KS + 2 * (16 * kk + 8 * half));
-        sacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, kv),
-                                                       __builtin_bit_cast(bf16x8_t, qop[kk]),
-                                                       sacc, 0, 0, 0);
-      }
-      // Scores of this lane's row: register i -> key k0 + 8(i/4) + 4 half + i%4.
-      float sc[16];
-      float tmax = -INFINITY;
+        const bf16x8_t qb = __builtin_bit_cast(bf16x8_t, qop[kk]);
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        float x = sacc[i] * p.score_scale;
-        if (p.has_cap) x = soft_cap_fn(x, p.cap, p.inv_cap);
-        x *= kLog2e;
-        const int32_t j = k0 + 8 * (i >> 2) + 4 * half + (i & 3);
-        x = (j >= row_lo && j < row_hi) ? x : -INFINITY;
-        sc[i] = x;
-        tmax = fmaxf(tmax, x);
-      }
-      tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
-      const float m_new = fmaxf(m_run, tmax);
-      // Rows with no valid key yet keep m = -inf and contribute nothing.
-      const float m_use = (m_new == -INFINITY) ? 0.0f : m_new;
-      const float alpha = (m_run == -INFINITY) ? 0.0f : exp2f(m_run - m_use);
-      float psum = 0.0f;
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        sc[i] = exp2f(sc[i] - m_use);  // exp2(-inf) = 0 for masked keys
-        psum += sc[i];
-      }
-      l_run = l_run * alpha + psum;
-      m_run = m_new;
-      // Rescale the output only when some row's max moved (wave-uniform test).
-      if (__any(alpha != 1.0f)) {
-#pragma unroll
-        for (int tt = 0; tt < C::NT; ++tt) oacc[tt] *= alpha;
-      }
-      // P^T operands: k-step ks from registers 8ks .. 8ks + 7.
-      uint4 pop[2];
-#pragma unroll
-      for (int ks = 0; ks < 2; ++ks)
-        pop[ks] = make_uint4(pack_bf16x2_rne(sc[8 * ks + 0], sc[8 * ks + 1]),
-                             pack_bf16x2_rne(sc[8 * ks + 2], sc[8 * ks + 3]),
-                             pack_bf16x2_rne(sc[8 * ks + 4], sc[8 * ks + 5]),
-                             pack_bf16x2_rne(sc[8 * ks + 6], sc[8 * ks + 7]));
-      // O^T += V^T . P^T.  V^T operand lane l -> dim 32tt + l % 32; k-slots
-      // 0..3 -> keys 16ks + 4 half + 0..3, slots 4..7 -> keys 16ks + 8 + 4 half
-      // + 0..3.  ds_read_b64_tr_b16 in 16-lane group G: source lane j points at
-      // key kbase + j / 4, dims d0 + 4 (j % 4); lane n receives
-      // V[kbase + 0..3][d0 + n].
-      const int G = lane >> 4, jl = lane & 15;
-#pragma unroll
-      for (int ks = 0; ks < 2; ++ks) {
-        const int key_a = 16 * ks + 4 * (G >> 1) + (jl >> 2);
-        const unsigned char* ra = vbuf + key_a * C::VS + 2 * (16 * (G & 1) + 4 * (jl & 3));
-        const unsigned char* rb = ra + 8 * C::VS;
-#pragma unroll
-        for (int tt = 0; tt < C::NT; ++tt) {
-          const v4i16 va = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-              (__attribute__((address_space(3))) v4i16*)(ra + 64 * tt));
-          const v4i16 vb = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-              (__attribute__((address_space(3))) v4i16*)(rb + 64 * tt));
-          const uint2 ua = __builtin_bit_cast(uint2, va), ub = __builtin_bit_cast(uint2, vb);
-          const uint4 vop = make_uint4(ua.x, ua.y, ub.x, ub.y);
-          oacc[tt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, vop),
-                                                             __builtin_bit_cast(bf16x8_t, pop[ks]),
-                                                             oacc[tt], 0, 0, 0);
+        for (int sb = 0; sb < C::NSB; ++sb) {
+          const uint4 kv = *reinterpret_cast<const uint4*>(
+              kbuf + (32 * sb + col) * C::KS + 2 * (16 * kk + 8 * half));
+          sacc[sb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, kv), qb,
+                                                             sacc[sb], 0, 0, 0);
         }
       }
+      // Scores y (raw logits, or soft-capped logits in log2 units); register i
+      // of block sb -> key k0 + 32 sb + 8(i/4) + 4 half + i%4.
+      float y[16 * C::NSB];
+#pragma unroll
+      for (int sb = 0; sb < C::NSB; ++sb)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          float x = sacc[sb][i];
+          if (p.has_cap) x = soft_cap_fn(x * p.score_scale, p.cap, p.inv_cap) * kLog2e;
+          y[16 * sb + i] = x;
+        }
+      // A non-positive multiplier is applied before masking (the max and the
+      // exp argument below assume cm > 0).
+      float cme = cm;
+      if (!(cm > 0.0f)) {
+#pragma unroll
+        for (int i = 0; i < 16 * C::NSB; ++i) y[i] *= cm;
+        cme = 1.0f;
+      }
+      // Masks only where some row of the wavefront does not see the whole tile.
+      if (!(k0 >= w_lo1 && k0 + BK <= w_hi0)) {
+#pragma unroll
+        for (int sb = 0; sb < C::NSB; ++sb)
+#pragma unroll
+          for (int i = 0; i < 16; ++i) {
+            const int32_t j = k0 + 32 * sb + 8 * (i >> 2) + 4 * half + (i & 3);
+            if (j < row_lo || j >= row_hi) y[16 * sb + i] = -INFINITY;
+          }
+      }
+      float tmax = -INFINITY;
+#pragma unroll
+      for (int i = 0; i < 16 * C::NSB; ++i) tmax = fmaxf(tmax, y[i]);
+      tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+      const float m_tile = tmax * cme;  // -inf stays -inf (cme > 0)
+      // Move the reference max only when it grew by more than 2^8 somewhere.
+      if (__any(m_tile > m_ref + kRescaleLog2)) {
+        const float m_new = fmaxf(m_ref, m_tile);
+        const float alpha = (m_ref == -INFINITY) ? 0.0f : exp2f(m_ref - m_new);
+        l_run *= alpha;
+#pragma unroll
+        for (int tt = 0; tt < C::NT; ++tt) oacc[tt] *= alpha;
+        m_ref = m_new;
+      }
+      const float m_use = (m_ref == -INFINITY) ? 0.0f : m_ref;
+      float psum = 0.0f;
+#pragma unroll
+      for (int i = 0; i < 16 * C::NSB; ++i) {
+        y[i] = __builtin_amdgcn_exp2f(fmaf(y[i], cme, -m_use));  // masked: exp2(-inf) = 0
+        psum += y[i];
+      }
+      l_run += psum;
+      // O^T += V^T . P^T.  P^T k-step (sb, ks) is registers 16 sb + 8 ks .. + 7;
+      // the V^T operand: lane l -> dim 32 tt + l % 32, k-slots 0..3 -> keys
+      // 32 sb + 16 ks + 4 half + 0..3, slots 4..7 -> the same + 8.
+      // ds_read_b64_tr_b16 in 16-lane group G: source lane j points at key
+      // kbase + j / 4, dims d0 + 4 (j % 4); lane n receives V[kbase + 0..3][d0 + n].
+      const int G = lane >> 4, jl = lane & 15;
+#pragma unroll
+      for (int sb = 0; sb < C::NSB; ++sb)
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) {
+          const float* pv = y + 16 * sb + 8 * ks;
+          const uint4 pop = make_uint4(pack_bf16x2_rne(pv[0], pv[1]), pack_bf16x2_rne(pv[2], pv[3]),
+                                       pack_bf16x2_rne(pv[4], pv[5]), pack_bf16x2_rne(pv[6], pv[7]));
+          const int key_a = 32 * sb + 16 * ks + 4 * (G >> 1) + (jl >> 2);
+          const unsigned char* ra = vbuf + key_a * C::VS + 2 * (16 * (G & 1) + 4 * (jl & 3));
+          const unsigned char* rb = ra + 8 * C::VS;
+#pragma unroll
+          for (int tt = 0; tt < C::NT; ++tt) {
+            const v4i16 va = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                (__attribute__((address_space(3))) v4i16*)(ra + 64 * tt));
+            const v4i16 vb = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                (__attribute__((address_space(3))) v4i16*)(rb + 64 * tt));
+            const uint2 ua = __builtin_bit_cast(uint2, va), ub = __builtin_bit_cast(uint2, vb);
+            const uint4 vop = make_uint4(ua.x, ua.y, ub.x, ub.y);
+            oacc[tt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, vop),
+                                                               __builtin_bit_cast(bf16x8_t, pop),
+                                                               oacc[tt], 0, 0, 0);
+          }
+        }
     }
     if (t + 1 < ntiles) store_tile(smem + ((t + 1) & 1) * C::BUF);
     __syncthreads();
