@@ -69,6 +69,13 @@ __device__ __forceinline__ uint32_t pack_bf16x2_rne(float lo, float hi) {
   return __builtin_bit_cast(uint32_t, r);
 }
 
+// Sum of a packed bf16 pair added to acc (v_dot2 with (1, 1)).
+__device__ __forceinline__ float sum_bf16x2(uint32_t pair, float acc) {
+  typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+  const bf16x2_t ones = {static_cast<__bf16>(1.0f), static_cast<__bf16>(1.0f)};
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, pair), ones, acc, false);
+}
+
 template <int DP>
 struct PrefillCfg {
   static constexpr int BK = DP == 128 ? 64 : 32;   // keys per tile
@@ -105,7 +112,8 @@ __device__ __forceinline__ int32_t prefill_blocks(const Params& p, const int32_t
 }
 
 // Two workgroups per CU at head_dim 128 (256 registers per lane), one at 256.
-template <typename KV, int DP, typename OutS>
+// FULL_D: head_dim == Dp (no zero-padded dims to skip).
+template <typename KV, int DP, typename OutS, bool FULL_D>
 __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(DP == 128 ? 2 : 1)))
 prefill_kernel(Params p, const uint16_t* __restrict__ q,
                const typename KV::storage* __restrict__ keys,
@@ -120,6 +128,8 @@ prefill_kernel(Params p, const uint16_t* __restrict__ q,
   __shared__ __align__(16) unsigned char smem[2 * C::BUF];
   __shared__ int32_t pages[kItemPages];
   __shared__ int32_t red[3 * kPlanWaves];
+  // Per-tile key address table, two tiles: [slot][key] = {K row, V row}.
+  __shared__ __align__(16) uint64_t ktab[2][BK][2];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -214,34 +224,44 @@ prefill_kernel(Params p, const uint16_t* __restrict__ q,
     }
   }
 
-  // ---- tile staging.  Thread tid always moves piece c = tid % PPK (K for
-  // c < Dp / 8, else V; elements e0 .. e0 + 7) of keys tid / PPK + KPI * i.
+  // ---- tile staging.  The address of every key's K and V row (its cache
+  // record, or its k/v input row for this call's new tokens) is computed
+  // once per tile by threads 0 .. BK-1, one tile ahead, into ktab.  Thread
+  // tid then always moves piece c = tid % PPK (K for c < Dp / 8, else V;
+  // elements e0 .. e0 + 7) of keys tid / PPK + KPI * i.
+  auto fill_tab = [&](int32_t t, int slot) __attribute__((always_inline)) {
+    if (tid < BK) {
+      const int32_t j = min(lo + t * BK + tid, hi - 1);  // past the range: a valid key
+      const E* kr;
+      const E* vr;
+      if (new_from_input && j >= new_start) {
+        const int64_t row = min(q_start + (j - new_start), p.T - 1);
+        kr = keys + (row * p.Hkv + h) * p.D;
+        vr = values + (row * p.Hkv + h) * p.D;
+      } else {
+        const int32_t pg = lds_pages ? pages[page_of(p, j) - pg0]
+                                     : min(max(ptab[page_of(p, j)], 0), p.P - 1);
+        kr = cache + (static_cast<int64_t>(pg) * p.ps + slot_of(p, j)) * p.rec +
+             static_cast<int64_t>(2 * h) * DP;
+        vr = kr + DP;
+      }
+      ktab[slot][tid][0] = reinterpret_cast<uint64_t>(kr);
+      ktab[slot][tid][1] = reinterpret_cast<uint64_t>(vr);
+    }
+  };
   const int pc = tid % C::PPK;
   const int pkey = tid / C::PPK;
   const int isv = pc >= DP / 8;
   const int e0 = (pc - isv * (DP / 8)) * 8;
-  const bool piece_live = e0 < p.D;
-  const E* in_base = (isv ? values : keys) + static_cast<int64_t>(h) * p.D + e0;
-  const int64_t cache_off = static_cast<int64_t>(2 * h + isv) * DP + e0;
+  const bool piece_live = FULL_D || e0 < p.D;
   uint4 stage[C::PPT];
   auto load_tile = [&](int32_t t) __attribute__((always_inline)) {
-    const int32_t k0 = lo + t * BK;
+    const int slot = t & 1;
 #pragma unroll
     for (int i = 0; i < C::PPT; ++i) {
-      const int32_t j = min(k0 + pkey + C::KPI * i, hi - 1);  // past the range: a valid key
+      const E* src = reinterpret_cast<const E*>(ktab[slot][pkey + C::KPI * i][isv]) + e0;
       uint4 v = make_uint4(0u, 0u, 0u, 0u);
-      if (piece_live) {
-        const E* src;
-        if (new_from_input && j >= new_start) {
-          const int64_t row = min(q_start + (j - new_start), p.T - 1);
-          src = in_base + row * p.Hkv * p.D;
-        } else {
-          const int32_t pg = lds_pages ? pages[page_of(p, j) - pg0]
-                                       : min(max(ptab[page_of(p, j)], 0), p.P - 1);
-          src = cache + (static_cast<int64_t>(pg) * p.ps + slot_of(p, j)) * p.rec + cache_off;
-        }
-        v = KV::load8(src);
-      }
+      if (piece_live) v = KV::load8(src);
       stage[i] = v;
     }
   };
@@ -261,6 +281,9 @@ prefill_kernel(Params p, const uint16_t* __restrict__ q,
   float m_ref = -INFINITY;  // reference max of the row (log2 units)
   float l_run = 0.0f;       // this lane's share of the row sum (relative to m_ref)
 
+  if (ntiles > 0) fill_tab(0, 0);
+  if (ntiles > 1) fill_tab(1, 1);
+  __syncthreads();
   if (ntiles > 0) {
     load_tile(0);
     store_tile(smem);
@@ -268,6 +291,8 @@ prefill_kernel(Params p, const uint16_t* __restrict__ q,
   __syncthreads();
   for (int32_t t = 0; t < ntiles; ++t) {
     if (t + 1 < ntiles) load_tile(t + 1);
+    // Slot t & 1 was last read by load_tile(t), before the previous barrier.
+    if (t + 2 < ntiles) fill_tab(t + 2, t & 1);
     const unsigned char* kbuf = smem + (t & 1) * C::BUF;
     const unsigned char* vbuf = kbuf + BK * C::KS;
     const int32_t k0 = lo + t * BK;
@@ -331,11 +356,20 @@ prefill_kernel(Params p, const uint16_t* __restrict__ q,
         m_ref = m_new;
       }
       const float m_use = (m_ref == -INFINITY) ? 0.0f : m_ref;
+#pragma unroll
+      for (int i = 0; i < 16 * C::NSB; ++i)
+        y[i] = __builtin_amdgcn_exp2f(fmaf(y[i], cme, -m_use));  // masked: exp2(-inf) = 0
+      // P^T operands (bf16, round to nearest even); the row sum adds the same
+      // rounded values the PV product uses (v_dot2 with (1, 1)).
+      uint4 pops[2 * C::NSB];
       float psum = 0.0f;
 #pragma unroll
-      for (int i = 0; i < 16 * C::NSB; ++i) {
-        y[i] = __builtin_amdgcn_exp2f(fmaf(y[i], cme, -m_use));  // masked: exp2(-inf) = 0
-        psum += y[i];
+      for (int q8 = 0; q8 < 2 * C::NSB; ++q8) {
+        const float* pv = y + 8 * q8;
+        pops[q8] = make_uint4(pack_bf16x2_rne(pv[0], pv[1]), pack_bf16x2_rne(pv[2], pv[3]),
+                              pack_bf16x2_rne(pv[4], pv[5]), pack_bf16x2_rne(pv[6], pv[7]));
+        psum = sum_bf16x2(pops[q8].x, sum_bf16x2(pops[q8].y, psum));
+        psum = sum_bf16x2(pops[q8].z, sum_bf16x2(pops[q8].w, psum));
       }
       l_run += psum;
       // O^T += V^T . P^T.  P^T k-step (sb, ks) is registers 16 sb + 8 ks .. + 7;
@@ -348,9 +382,7 @@ prefill_kernel(Params p, const uint16_t* __restrict__ q,
       for (int sb = 0; sb < C::NSB; ++sb)
 #pragma unroll
         for (int ks = 0; ks < 2; ++ks) {
-          const float* pv = y + 16 * sb + 8 * ks;
-          const uint4 pop = make_uint4(pack_bf16x2_rne(pv[0], pv[1]), pack_bf16x2_rne(pv[2], pv[3]),
-                                       pack_bf16x2_rne(pv[4], pv[5]), pack_bf16x2_rne(pv[6], pv[7]));
+          const uint4 pop = pops[2 * sb + ks];
           const int key_a = 32 * sb + 16 * ks + 4 * (G >> 1) + (jl >> 2);
           const unsigned char* ra = vbuf + key_a * C::VS + 2 * (16 * (G & 1) + 4 * (jl & 3));
           const unsigned char* rb = ra + 8 * C::VS;
@@ -408,15 +440,16 @@ hipError_t launch_dp(const Params& p, const void* q, const void* k, const void* 
   const int64_t grid = blocks * p.Hkv;
   if (grid > 0x7fffffff) return hipErrorInvalidValue;
   const dim3 g(static_cast<uint32_t>(grid)), blk(kThreads);
-#define RPA_PREFILL_LAUNCH(DPV)                                                              \
-  hipLaunchKernelGGL((prefill_kernel<KV, DPV, OutS>), g, blk, 0, stream, p,                 \
+#define RPA_PREFILL_LAUNCH(DPV, FULL)                                                        \
+  hipLaunchKernelGGL((prefill_kernel<KV, DPV, OutS, FULL>), g, blk, 0, stream, p,           \
                      static_cast<const uint16_t*>(q), static_cast<const E*>(k),             \
                      static_cast<const E*>(v), static_cast<const E*>(cache), kv_lens,       \
                      page_indices, cu, dist, static_cast<OutS*>(out))
+  const bool full = p.D == p.Dp;
   if (p.Dp == 128) {
-    RPA_PREFILL_LAUNCH(128);
+    if (full) RPA_PREFILL_LAUNCH(128, true); else RPA_PREFILL_LAUNCH(128, false);
   } else if (p.Dp == 256) {
-    RPA_PREFILL_LAUNCH(256);
+    if (full) RPA_PREFILL_LAUNCH(256, true); else RPA_PREFILL_LAUNCH(256, false);
   } else {
     return hipErrorInvalidValue;
   }
