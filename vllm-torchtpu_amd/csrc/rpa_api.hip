@@ -206,7 +206,7 @@ int rpa_forward(const rpa_desc* d, const void* queries, const void* keys, const 
   if (rpa::prefill_supported(p, d->q_dtype, d->kv_dtype, d->out_dtype)) {
     hipError_t e = rpa::launch_prefill(p, d->kv_dtype, d->out_dtype, queries, keys, values,
                                        kv_cache, kv_lens, page_indices, cu_q_lens, distribution,
-                                       out, s);
+                                       out, ws.plan, s);
     if (e != hipSuccess) return RPA_ERR_LAUNCH;
     p.prefill_on = 1;
   }

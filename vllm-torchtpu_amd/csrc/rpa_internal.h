@@ -28,7 +28,7 @@ struct DecodeWorkspace {
 
 
 // Plan written by the decode kernel: [0] num_seqs n, [1] tiles per unit,
-// [2] total units, [3] unused; units[S + 1] (exclusive prefix, units[n] =
+// [2] total units, [3] sequences with non-decode rows; units[S + 1] (exclusive prefix, units[n] =
 // total), dkv[S] (kv_len of a decode sequence, else 0), tq[S] (q row of the
 // sequence), rowseq[T] (sequence of a token row the finish kernel owns, -1 for
 // decode rows and padding rows).
@@ -67,11 +67,13 @@ hipError_t launch_decode(const Params& p, int kv_dtype, int out_dtype, const Dec
 // Prefill kernel: MFMA attention of every row the decode kernel does not
 // take (new tokens read from k/v; their cache write is the finish kernel's).
 bool prefill_supported(const Params& p, int q_dtype, int kv_dtype, int out_dtype);
+// With the decode kernel on (p.decode_waves > 0) `plan` is its published
+// plan, and a batch without non-decode rows ends the launch at once.
 hipError_t launch_prefill(const Params& p, int kv_dtype, int out_dtype, const void* q,
                           const void* k, const void* v, const void* cache,
                           const int32_t* kv_lens, const int32_t* page_indices,
                           const int32_t* cu, const int32_t* dist, void* out,
-                          hipStream_t stream);
+                          const int32_t* plan, hipStream_t stream);
 
 // Finish kernel: merges the decode partials, writes the new tokens of every
 // non-decode row into the cache and, unless p.prefill_on, attends those rows

@@ -191,7 +191,7 @@ __device__ __forceinline__ void publish_plan(const Params& p, const Plan& pl, co
       plan[0] = n;
       plan[1] = pl.tpu;
       plan[2] = pl.total_units;
-      plan[3] = 0;
+      plan[3] = pl.n_other;
     }
     for (int32_t s = tid; s <= n; s += kPlanThreads) units[s] = L.units[s];
     for (int32_t s = tid; s < n; s += kPlanThreads) {

@@ -121,7 +121,7 @@ prefill_kernel(Params p, const uint16_t* __restrict__ q,
                const typename KV::storage* __restrict__ cache,
                const int32_t* __restrict__ kv_lens, const int32_t* __restrict__ page_indices,
                const int32_t* __restrict__ cu, const int32_t* __restrict__ dist,
-               OutS* __restrict__ out) {
+               OutS* __restrict__ out, const int32_t* __restrict__ plan) {
   using C = PrefillCfg<DP>;
   using E = typename KV::storage;
   constexpr int BK = C::BK;
@@ -138,6 +138,8 @@ prefill_kernel(Params p, const uint16_t* __restrict__ q,
   const int half = lane >> 5;
   const bool decode_on = p.decode_waves > 0;
   const int32_t bq = kRows / p.qpk;  // query tokens per item
+  // The decode kernel counted the sequences with non-decode rows.
+  if (decode_on && plan[3] == 0) return;
 
   // ---- item: (block kb over all owned sequences, kv head h).  The block
   // prefix lives in the (not yet used) tile buffers.
@@ -288,6 +290,11 @@ prefill_kernel(Params p, const uint16_t* __restrict__ q,
     load_tile(0);
     store_tile(smem);
   }
+  // Every load issued so far (the q operand included) completes here, so no
+  // load from before the loop is still pending inside it: otherwise each
+  // iteration would wait for all loads -- the next tile's prefetch too --
+  // before its first use of the q operand.
+  __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
   for (int32_t t = 0; t < ntiles; ++t) {
     if (t + 1 < ntiles) load_tile(t + 1);
@@ -432,7 +439,8 @@ prefill_kernel(Params p, const uint16_t* __restrict__ q,
 template <typename KV, typename OutS>
 hipError_t launch_dp(const Params& p, const void* q, const void* k, const void* v,
                      const void* cache, const int32_t* kv_lens, const int32_t* page_indices,
-                     const int32_t* cu, const int32_t* dist, void* out, hipStream_t stream) {
+                     const int32_t* cu, const int32_t* dist, void* out, const int32_t* plan,
+                     hipStream_t stream) {
   using E = typename KV::storage;
   // Upper bound on items: every sequence adds at most one partial block.
   const int32_t bq = kRows / p.qpk;
@@ -444,7 +452,7 @@ hipError_t launch_dp(const Params& p, const void* q, const void* k, const void* 
   hipLaunchKernelGGL((prefill_kernel<KV, DPV, OutS, FULL>), g, blk, 0, stream, p,           \
                      static_cast<const uint16_t*>(q), static_cast<const E*>(k),             \
                      static_cast<const E*>(v), static_cast<const E*>(cache), kv_lens,       \
-                     page_indices, cu, dist, static_cast<OutS*>(out))
+                     page_indices, cu, dist, static_cast<OutS*>(out), plan)
   const bool full = p.D == p.Dp;
   if (p.Dp == 128) {
     if (full) RPA_PREFILL_LAUNCH(128, true); else RPA_PREFILL_LAUNCH(128, false);
@@ -460,14 +468,15 @@ hipError_t launch_dp(const Params& p, const void* q, const void* k, const void* 
 template <typename OutS>
 hipError_t launch_kv(const Params& p, int kv_dtype, const void* q, const void* k, const void* v,
                      const void* cache, const int32_t* kv_lens, const int32_t* page_indices,
-                     const int32_t* cu, const int32_t* dist, void* out, hipStream_t stream) {
+                     const int32_t* cu, const int32_t* dist, void* out, const int32_t* plan,
+                     hipStream_t stream) {
   switch (kv_dtype) {
     case RPA_DTYPE_BF16:
-      return launch_dp<PKvBF16, OutS>(p, q, k, v, cache, kv_lens, page_indices, cu, dist, out, stream);
+      return launch_dp<PKvBF16, OutS>(p, q, k, v, cache, kv_lens, page_indices, cu, dist, out, plan, stream);
     case RPA_DTYPE_FP8_E4M3FN:
-      return launch_dp<PKvFP8<false>, OutS>(p, q, k, v, cache, kv_lens, page_indices, cu, dist, out, stream);
+      return launch_dp<PKvFP8<false>, OutS>(p, q, k, v, cache, kv_lens, page_indices, cu, dist, out, plan, stream);
     case RPA_DTYPE_FP8_E5M2:
-      return launch_dp<PKvFP8<true>, OutS>(p, q, k, v, cache, kv_lens, page_indices, cu, dist, out, stream);
+      return launch_dp<PKvFP8<true>, OutS>(p, q, k, v, cache, kv_lens, page_indices, cu, dist, out, plan, stream);
     default:
       return hipErrorInvalidValue;
   }
@@ -492,10 +501,11 @@ hipError_t launch_prefill(const Params& p, int kv_dtype, int out_dtype, const vo
                           const void* k, const void* v, const void* cache,
                           const int32_t* kv_lens, const int32_t* page_indices,
                           const int32_t* cu, const int32_t* dist, void* out,
-                          hipStream_t stream) {
+                          const int32_t* plan, hipStream_t stream) {
+  if (p.decode_waves > 0 && plan == nullptr) return hipErrorInvalidValue;
   if (out_dtype == RPA_DTYPE_F32)
-    return launch_kv<float>(p, kv_dtype, q, k, v, cache, kv_lens, page_indices, cu, dist, out, stream);
-  return launch_kv<uint16_t>(p, kv_dtype, q, k, v, cache, kv_lens, page_indices, cu, dist, out, stream);
+    return launch_kv<float>(p, kv_dtype, q, k, v, cache, kv_lens, page_indices, cu, dist, out, plan, stream);
+  return launch_kv<uint16_t>(p, kv_dtype, q, k, v, cache, kv_lens, page_indices, cu, dist, out, plan, stream);
 }
 
 }  // namespace rpa
