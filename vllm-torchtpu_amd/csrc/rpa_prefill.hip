@@ -40,22 +40,24 @@ typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
 typedef short v4i16 __attribute__((ext_vector_type(4)));
 
-constexpr int kThreads = 256;
-constexpr int kRows = 128;  // q rows per item (32 per wavefront)
 constexpr float kLog2e = 1.4426950408889634f;
 
 // KV element types: 8 elements per load piece, converted to 8 bf16.
+// Loads through global (address space 1) pointers, as native vectors.
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
 struct PKvBF16 {
   using storage = uint16_t;
-  static __device__ __forceinline__ uint4 load8(const storage* p) {
-    return *reinterpret_cast<const uint4*>(p);
+  static __device__ __forceinline__ uint4 load8g(const __attribute__((address_space(1))) storage* p) {
+    const u32x4_t r = *reinterpret_cast<const __attribute__((address_space(1))) u32x4_t*>(p);
+    return make_uint4(r.x, r.y, r.z, r.w);
   }
 };
 template <bool kE5M2>
 struct PKvFP8 {
   using storage = uint8_t;
-  static __device__ __forceinline__ uint4 load8(const storage* p) {
-    const uint2 r = *reinterpret_cast<const uint2*>(p);
+  static __device__ __forceinline__ uint4 load8g(const __attribute__((address_space(1))) storage* p) {
+    const u32x2_t r = *reinterpret_cast<const __attribute__((address_space(1))) u32x2_t*>(p);
     const uint2 a = fp8x4_to_bf16x4<kE5M2>(r.x), b = fp8x4_to_bf16x4<kE5M2>(r.y);
     return make_uint4(a.x, a.y, b.x, b.y);
   }
@@ -78,17 +80,21 @@ __device__ __forceinline__ float sum_bf16x2(uint32_t pair, float acc) {
 
 template <int DP>
 struct PrefillCfg {
+  // 4 wavefronts: two workgroups per CU at head_dim 128, one at 256.
+  static constexpr int THREADS = 256;
+  static constexpr int ROWS = 32 * THREADS / 64;   // q rows per item (32 per wavefront)
   static constexpr int BK = DP == 128 ? 64 : 32;   // keys per tile
   static constexpr int NSB = BK / 32;              // 32-key S^T blocks per tile
   static constexpr int KS = 2 * DP + 16;           // LDS K row stride (bytes)
   static constexpr int VS = 2 * DP + 32;           // LDS V row stride (bytes)
   static constexpr int BUF = BK * (KS + VS);       // one K|V tile buffer
   static constexpr int PPK = 2 * DP / 8;           // 8-element pieces per key (K then V)
-  static constexpr int KPI = kThreads / PPK;       // keys covered per staging step
+  static constexpr int KPI = THREADS / PPK;        // keys covered per staging step
   static constexpr int PPT = BK / KPI;             // pieces per thread per tile
   static constexpr int KSTEPS = DP / 16;           // QK^T k-steps over head_dim
   static constexpr int NT = DP / 32;               // 32-dim output blocks
-  static_assert(kThreads % PPK == 0 && BK % KPI == 0, "whole pieces per thread");
+  static_assert(THREADS % PPK == 0 && BK % KPI == 0, "whole pieces per thread");
+  static_assert(THREADS >= kPlanThreads && 3 * kPlanWaves >= THREADS / 64, "plan scan fits");
   static_assert(2 * BUF >= 4 * (kMaxDecodeSeqs + 1), "plan scratch fits the tile buffers");
 };
 
@@ -114,7 +120,7 @@ __device__ __forceinline__ int32_t prefill_blocks(const Params& p, const int32_t
 // Two workgroups per CU at head_dim 128 (256 registers per lane), one at 256.
 // FULL_D: head_dim == Dp (no zero-padded dims to skip).
 template <typename KV, int DP, typename OutS, bool FULL_D>
-__global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(DP == 128 ? 2 : 1)))
+__global__ void __launch_bounds__(PrefillCfg<DP>::THREADS) __attribute__((amdgpu_waves_per_eu(DP == 128 ? 2 : 1)))
 prefill_kernel(Params p, const uint16_t* __restrict__ q,
                const typename KV::storage* __restrict__ keys,
                const typename KV::storage* __restrict__ values,
@@ -128,8 +134,8 @@ prefill_kernel(Params p, const uint16_t* __restrict__ q,
   __shared__ __align__(16) unsigned char smem[2 * C::BUF];
   __shared__ int32_t pages[kItemPages];
   __shared__ int32_t red[3 * kPlanWaves];
-  // Per-tile key address table, two tiles: [slot][key] = {K row, V row}.
-  __shared__ __align__(16) uint64_t ktab[2][BK][2];
+  // Key address table, three tiles: [t % 3][key] = {K row, V row}.
+  __shared__ __align__(16) uint64_t ktab[3][BK][2];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -137,7 +143,7 @@ prefill_kernel(Params p, const uint16_t* __restrict__ q,
   const int col = lane & 31;  // MFMA column: this lane's q row within the wavefront
   const int half = lane >> 5;
   const bool decode_on = p.decode_waves > 0;
-  const int32_t bq = kRows / p.qpk;  // query tokens per item
+  const int32_t bq = C::ROWS / p.qpk;  // query tokens per item
   // The decode kernel counted the sequences with non-decode rows.
   if (decode_on && plan[3] == 0) return;
 
@@ -145,7 +151,7 @@ prefill_kernel(Params p, const uint16_t* __restrict__ q,
   // prefix lives in the (not yet used) tile buffers.
   int32_t* blk = reinterpret_cast<int32_t*>(smem);
   const int32_t n = min(num_seqs_of(dist, p.S), kMaxDecodeSeqs);
-  for (int32_t s = tid; s < n; s += kThreads)
+  for (int32_t s = tid; s < n; s += C::THREADS)
     blk[s] = prefill_blocks(p, cu, kv_lens, s, bq, decode_on);
   __syncthreads();
   block_exclusive_scan(blk, n, red);
@@ -211,7 +217,7 @@ prefill_kernel(Params p, const uint16_t* __restrict__ q,
   const int32_t npg = hi > lo ? page_of(p, hi - 1) - pg0 + 1 : 0;
   const bool lds_pages = npg <= kItemPages;
   if (lds_pages)
-    for (int32_t i = tid; i < npg; i += kThreads) pages[i] = min(max(ptab[pg0 + i], 0), p.P - 1);
+    for (int32_t i = tid; i < npg; i += C::THREADS) pages[i] = min(max(ptab[pg0 + i], 0), p.P - 1);
   __syncthreads();  // the plan scratch is dead; the page ids are visible
 
   // ---- Q^T operand (B of S^T): column = row, k-slots 8 * half .. + 7 of
@@ -228,9 +234,10 @@ prefill_kernel(Params p, const uint16_t* __restrict__ q,
 
   // ---- tile staging.  The address of every key's K and V row (its cache
   // record, or its k/v input row for this call's new tokens) is computed
-  // once per tile by threads 0 .. BK-1, one tile ahead, into ktab.  Thread
-  // tid then always moves piece c = tid % PPK (K for c < Dp / 8, else V;
-  // elements e0 .. e0 + 7) of keys tid / PPK + KPI * i.
+  // once per tile by threads 0 .. BK-1, three tiles ahead, into ktab.  Thread
+  // tid always moves piece c = tid % PPK (K for c < Dp / 8, else V; elements
+  // e0 .. e0 + 7) of keys tid / PPK + KPI * i.  Tile loads are issued two
+  // tiles ahead into two register stages.
   auto fill_tab = [&](int32_t t, int slot) __attribute__((always_inline)) {
     if (tid < BK) {
       const int32_t j = min(lo + t * BK + tid, hi - 1);  // past the range: a valid key
@@ -256,18 +263,22 @@ prefill_kernel(Params p, const uint16_t* __restrict__ q,
   const int isv = pc >= DP / 8;
   const int e0 = (pc - isv * (DP / 8)) * 8;
   const bool piece_live = FULL_D || e0 < p.D;
-  uint4 stage[C::PPT];
-  auto load_tile = [&](int32_t t) __attribute__((always_inline)) {
-    const int slot = t & 1;
+  // The table holds plain addresses; they are global memory, so the loads are
+  // global (not flat) loads and count only against vmcnt -- a flat load would
+  // also hold up every LDS wait of the compute phase.
+  typedef const __attribute__((address_space(1))) E* GlobalPtr;
+  auto load_tile = [&](int32_t t, uint4* stage) __attribute__((always_inline)) {
+    const int slot = t % 3;
 #pragma unroll
     for (int i = 0; i < C::PPT; ++i) {
-      const E* src = reinterpret_cast<const E*>(ktab[slot][pkey + C::KPI * i][isv]) + e0;
+      const GlobalPtr src =
+          reinterpret_cast<GlobalPtr>(ktab[slot][pkey + C::KPI * i][isv]) + e0;
       uint4 v = make_uint4(0u, 0u, 0u, 0u);
-      if (piece_live) v = KV::load8(src);
+      if (piece_live) v = KV::load8g(src);
       stage[i] = v;
     }
   };
-  auto store_tile = [&](unsigned char* buf) __attribute__((always_inline)) {
+  auto store_tile = [&](unsigned char* buf, const uint4* stage) __attribute__((always_inline)) {
     unsigned char* dst0 = isv ? buf + BK * C::KS + pkey * C::VS + 2 * e0
                               : buf + pkey * C::KS + 2 * e0;
     const int rstride = isv ? C::VS : C::KS;
@@ -283,113 +294,107 @@ prefill_kernel(Params p, const uint16_t* __restrict__ q,
   float m_ref = -INFINITY;  // reference max of the row (log2 units)
   float l_run = 0.0f;       // this lane's share of the row sum (relative to m_ref)
 
-  if (ntiles > 0) fill_tab(0, 0);
-  if (ntiles > 1) fill_tab(1, 1);
-  __syncthreads();
-  if (ntiles > 0) {
-    load_tile(0);
-    store_tile(smem);
-  }
-  // Every load issued so far (the q operand included) completes here, so no
-  // load from before the loop is still pending inside it: otherwise each
-  // iteration would wait for all loads -- the next tile's prefetch too --
-  // before its first use of the q operand.
-  __builtin_amdgcn_s_waitcnt(0);
-  __syncthreads();
-  for (int32_t t = 0; t < ntiles; ++t) {
-    if (t + 1 < ntiles) load_tile(t + 1);
-    // Slot t & 1 was last read by load_tile(t), before the previous barrier.
-    if (t + 2 < ntiles) fill_tab(t + 2, t & 1);
+  // Attention of tile t (in LDS buffer t & 1).
+  auto compute_tile = [&](int32_t t) __attribute__((always_inline)) {
     const unsigned char* kbuf = smem + (t & 1) * C::BUF;
     const unsigned char* vbuf = kbuf + BK * C::KS;
     const int32_t k0 = lo + t * BK;
-    if (wave_live && k0 < w_hi1 && k0 + BK > w_lo0) {
-      // S^T = K . Q^T per 32-key block: A lane l -> key l % 32, dims 16kk + 8 half ..
+    if (!(wave_live && k0 < w_hi1 && k0 + BK > w_lo0)) return;
+    {
+      // S^T = K . Q^T per 32-key sub-block (A lane l -> key l % 32, dims
+      // 16kk + 8 half ..), sub-block-major: sub-block 0's scores are final
+      // while sub-block 1's MFMAs still run, so its softmax (VALU) overlaps
+      // them; likewise sub-block 1's softmax overlaps sub-block 0's PV MFMAs.
       f32x16_t sacc[C::NSB];
 #pragma unroll
-      for (int sb = 0; sb < C::NSB; ++sb) sacc[sb] = f32x16_t{};
+      for (int sb = 0; sb < C::NSB; ++sb) {
+        sacc[sb] = f32x16_t{};
 #pragma unroll
-      for (int kk = 0; kk < C::KSTEPS; ++kk) {
-        const bf16x8_t qb = __builtin_bit_cast(bf16x8_t, qop[kk]);
-#pragma unroll
-        for (int sb = 0; sb < C::NSB; ++sb) {
+        for (int kk = 0; kk < C::KSTEPS; ++kk) {
           const uint4 kv = *reinterpret_cast<const uint4*>(
               kbuf + (32 * sb + col) * C::KS + 2 * (16 * kk + 8 * half));
-          sacc[sb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, kv), qb,
-                                                             sacc[sb], 0, 0, 0);
+          sacc[sb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+              __builtin_bit_cast(bf16x8_t, kv), __builtin_bit_cast(bf16x8_t, qop[kk]), sacc[sb],
+              0, 0, 0);
         }
       }
-      // Scores y (raw logits, or soft-capped logits in log2 units); register i
-      // of block sb -> key k0 + 32 sb + 8(i/4) + 4 half + i%4.
-      float y[16 * C::NSB];
+      // Schedule: the K operand reads run four MFMAs ahead of their use (LDS
+      // latency is several MFMA durations).
+      constexpr int kS = C::NSB * C::KSTEPS;  // S^T MFMAs (and K reads) per tile
+      __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
 #pragma unroll
-      for (int sb = 0; sb < C::NSB; ++sb)
+      for (int i = 0; i < kS - 4; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      }
+      __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
+      // Masks only where some row of the wavefront does not see the whole tile.
+      const bool need_mask = !(k0 >= w_lo1 && k0 + BK <= w_hi0);
+      const int G = lane >> 4, jl = lane & 15;
+#pragma unroll
+      for (int sb = 0; sb < C::NSB; ++sb) {
+        // Scores y (raw logits, or soft-capped logits in log2 units); register
+        // i -> key k0 + 32 sb + 8(i/4) + 4 half + i%4.
+        float y[16];
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
           float x = sacc[sb][i];
           if (p.has_cap) x = soft_cap_fn(x * p.score_scale, p.cap, p.inv_cap) * kLog2e;
-          y[16 * sb + i] = x;
+          y[i] = x;
         }
-      // A non-positive multiplier is applied before masking (the max and the
-      // exp argument below assume cm > 0).
-      float cme = cm;
-      if (!(cm > 0.0f)) {
+        // A non-positive multiplier is applied before masking (the max and
+        // the exp argument below assume cme > 0).
+        float cme = cm;
+        if (!(cm > 0.0f)) {
 #pragma unroll
-        for (int i = 0; i < 16 * C::NSB; ++i) y[i] *= cm;
-        cme = 1.0f;
-      }
-      // Masks only where some row of the wavefront does not see the whole tile.
-      if (!(k0 >= w_lo1 && k0 + BK <= w_hi0)) {
-#pragma unroll
-        for (int sb = 0; sb < C::NSB; ++sb)
+          for (int i = 0; i < 16; ++i) y[i] *= cm;
+          cme = 1.0f;
+        }
+        if (need_mask) {
 #pragma unroll
           for (int i = 0; i < 16; ++i) {
             const int32_t j = k0 + 32 * sb + 8 * (i >> 2) + 4 * half + (i & 3);
-            if (j < row_lo || j >= row_hi) y[16 * sb + i] = -INFINITY;
+            if (j < row_lo || j >= row_hi) y[i] = -INFINITY;
           }
-      }
-      float tmax = -INFINITY;
+        }
+        float tmax = -INFINITY;
 #pragma unroll
-      for (int i = 0; i < 16 * C::NSB; ++i) tmax = fmaxf(tmax, y[i]);
-      tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
-      const float m_tile = tmax * cme;  // -inf stays -inf (cme > 0)
-      // Move the reference max only when it grew by more than 2^8 somewhere.
-      if (__any(m_tile > m_ref + kRescaleLog2)) {
-        const float m_new = fmaxf(m_ref, m_tile);
-        const float alpha = (m_ref == -INFINITY) ? 0.0f : exp2f(m_ref - m_new);
-        l_run *= alpha;
+        for (int i = 0; i < 16; ++i) tmax = fmaxf(tmax, y[i]);
+        tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+        const float m_tile = tmax * cme;  // -inf stays -inf (cme > 0)
+        // Move the reference max only when it grew by more than 2^8 somewhere.
+        if (__any(m_tile > m_ref + kRescaleLog2)) {
+          const float m_new = fmaxf(m_ref, m_tile);
+          const float alpha = (m_ref == -INFINITY) ? 0.0f : exp2f(m_ref - m_new);
+          l_run *= alpha;
 #pragma unroll
-        for (int tt = 0; tt < C::NT; ++tt) oacc[tt] *= alpha;
-        m_ref = m_new;
-      }
-      const float m_use = (m_ref == -INFINITY) ? 0.0f : m_ref;
+          for (int tt = 0; tt < C::NT; ++tt) oacc[tt] *= alpha;
+          m_ref = m_new;
+        }
+        const float m_use = (m_ref == -INFINITY) ? 0.0f : m_ref;
 #pragma unroll
-      for (int i = 0; i < 16 * C::NSB; ++i)
-        y[i] = __builtin_amdgcn_exp2f(fmaf(y[i], cme, -m_use));  // masked: exp2(-inf) = 0
-      // P^T operands (bf16, round to nearest even); the row sum adds the same
-      // rounded values the PV product uses (v_dot2 with (1, 1)).
-      uint4 pops[2 * C::NSB];
-      float psum = 0.0f;
-#pragma unroll
-      for (int q8 = 0; q8 < 2 * C::NSB; ++q8) {
-        const float* pv = y + 8 * q8;
-        pops[q8] = make_uint4(pack_bf16x2_rne(pv[0], pv[1]), pack_bf16x2_rne(pv[2], pv[3]),
-                              pack_bf16x2_rne(pv[4], pv[5]), pack_bf16x2_rne(pv[6], pv[7]));
-        psum = sum_bf16x2(pops[q8].x, sum_bf16x2(pops[q8].y, psum));
-        psum = sum_bf16x2(pops[q8].z, sum_bf16x2(pops[q8].w, psum));
-      }
-      l_run += psum;
-      // O^T += V^T . P^T.  P^T k-step (sb, ks) is registers 16 sb + 8 ks .. + 7;
-      // the V^T operand: lane l -> dim 32 tt + l % 32, k-slots 0..3 -> keys
-      // 32 sb + 16 ks + 4 half + 0..3, slots 4..7 -> the same + 8.
-      // ds_read_b64_tr_b16 in 16-lane group G: source lane j points at key
-      // kbase + j / 4, dims d0 + 4 (j % 4); lane n receives V[kbase + 0..3][d0 + n].
-      const int G = lane >> 4, jl = lane & 15;
-#pragma unroll
-      for (int sb = 0; sb < C::NSB; ++sb)
+        for (int i = 0; i < 16; ++i)
+          y[i] = __builtin_amdgcn_exp2f(fmaf(y[i], cme, -m_use));  // masked: exp2(-inf) = 0
+        // P^T operands (bf16, round to nearest even); the row sum adds the
+        // same rounded values the PV product uses (v_dot2 with (1, 1)).
+        uint4 pops[2];
+        float psum = 0.0f;
 #pragma unroll
         for (int ks = 0; ks < 2; ++ks) {
-          const uint4 pop = pops[2 * sb + ks];
+          const float* pv = y + 8 * ks;
+          pops[ks] = make_uint4(pack_bf16x2_rne(pv[0], pv[1]), pack_bf16x2_rne(pv[2], pv[3]),
+                                pack_bf16x2_rne(pv[4], pv[5]), pack_bf16x2_rne(pv[6], pv[7]));
+          psum = sum_bf16x2(pops[ks].x, sum_bf16x2(pops[ks].y, psum));
+          psum = sum_bf16x2(pops[ks].z, sum_bf16x2(pops[ks].w, psum));
+        }
+        l_run += psum;
+        // O^T += V^T . P^T.  P^T k-step ks is registers 8 ks .. + 7; the V^T
+        // operand: lane l -> dim 32 tt + l % 32, k-slots 0..3 -> keys
+        // 32 sb + 16 ks + 4 half + 0..3, slots 4..7 -> the same + 8.
+        // ds_read_b64_tr_b16 in 16-lane group G: source lane j points at key
+        // kbase + j / 4, dims d0 + 4 (j % 4); lane n receives V[kbase + 0..3][d0 + n].
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) {
           const int key_a = 32 * sb + 16 * ks + 4 * (G >> 1) + (jl >> 2);
           const unsigned char* ra = vbuf + key_a * C::VS + 2 * (16 * (G & 1) + 4 * (jl & 3));
           const unsigned char* rb = ra + 8 * C::VS;
@@ -401,14 +406,56 @@ prefill_kernel(Params p, const uint16_t* __restrict__ q,
                 (__attribute__((address_space(3))) v4i16*)(rb + 64 * tt));
             const uint2 ua = __builtin_bit_cast(uint2, va), ub = __builtin_bit_cast(uint2, vb);
             const uint4 vop = make_uint4(ua.x, ua.y, ub.x, ub.y);
-            oacc[tt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, vop),
-                                                               __builtin_bit_cast(bf16x8_t, pop),
-                                                               oacc[tt], 0, 0, 0);
+            oacc[tt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+                __builtin_bit_cast(bf16x8_t, vop), __builtin_bit_cast(bf16x8_t, pops[ks]),
+                oacc[tt], 0, 0, 0);
           }
         }
+        // Schedule: the V^T reads (two per MFMA) run two MFMAs ahead.
+        constexpr int kP = 2 * C::NT;  // PV MFMAs per sub-block
+        __builtin_amdgcn_sched_group_barrier(0x100, 4, 1);
+#pragma unroll
+        for (int i = 0; i < kP - 2; ++i) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);
+          __builtin_amdgcn_sched_group_barrier(0x100, 2, 1);
+        }
+        __builtin_amdgcn_sched_group_barrier(0x008, 2, 1);
+      }
     }
-    if (t + 1 < ntiles) store_tile(smem + ((t + 1) & 1) * C::BUF);
+  };
+
+  // ---- pipeline: iteration t issues the loads of tile t + 2 (register
+  // stage t & 1) and the address table of tile t + 3, computes tile t, then
+  // stores tile t + 1 (stage (t + 1) & 1) into LDS buffer (t + 1) & 1.
+  uint4 stage0[C::PPT], stage1[C::PPT];
+  // Every slot gets valid addresses (tiles past the end repeat the last
+  // one), so the unconditional prefetch below never reads an unset entry.
+  if (ntiles > 0)
+    for (int i = 0; i < 3; ++i) fill_tab(min(i, ntiles - 1), i);
+  __syncthreads();
+  if (ntiles > 0) load_tile(0, stage0);
+  if (ntiles > 1) load_tile(1, stage1);
+  if (ntiles > 0) store_tile(smem, stage0);
+  // Every load issued so far (the q operand included) completes here, so no
+  // load from before the loop is still pending inside it: otherwise each
+  // iteration would wait for all loads -- the prefetched tiles too -- before
+  // its first use of the q operand.
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  auto iter = [&](int32_t t, uint4* st_t, uint4* st_t1) __attribute__((always_inline)) {
+    // st_t held tile t (already in LDS); it now receives tile t + 2.  The
+    // load is unconditional (past the end: a re-read of the last tile, never
+    // stored), so the wait before storing st_t1 counts exactly these loads.
+    load_tile(min(t + 2, ntiles - 1), st_t);
+    // Slot t % 3 was last read by load_tile(t), two barriers ago.
+    if (t + 3 < ntiles) fill_tab(t + 3, t % 3);
+    compute_tile(t);
+    if (t + 1 < ntiles) store_tile(smem + ((t + 1) & 1) * C::BUF, st_t1);
     __syncthreads();
+  };
+  for (int32_t t = 0; t < ntiles; t += 2) {
+    iter(t, stage0, stage1);
+    if (t + 1 < ntiles) iter(t + 1, stage1, stage0);
   }
 
   // ---- output: lane l, block tt, register i -> dim 32tt + 8(i/4) + 4 half + i%4.
@@ -443,13 +490,14 @@ hipError_t launch_dp(const Params& p, const void* q, const void* k, const void* 
                      hipStream_t stream) {
   using E = typename KV::storage;
   // Upper bound on items: every sequence adds at most one partial block.
-  const int32_t bq = kRows / p.qpk;
+  const int32_t bq = (p.Dp == 128 ? PrefillCfg<128>::ROWS : PrefillCfg<256>::ROWS) / p.qpk;
   const int64_t blocks = (static_cast<int64_t>(p.T) + bq - 1) / bq + p.S;
   const int64_t grid = blocks * p.Hkv;
   if (grid > 0x7fffffff) return hipErrorInvalidValue;
-  const dim3 g(static_cast<uint32_t>(grid)), blk(kThreads);
+  const dim3 g(static_cast<uint32_t>(grid));
 #define RPA_PREFILL_LAUNCH(DPV, FULL)                                                        \
-  hipLaunchKernelGGL((prefill_kernel<KV, DPV, OutS, FULL>), g, blk, 0, stream, p,           \
+  hipLaunchKernelGGL((prefill_kernel<KV, DPV, OutS, FULL>), g,                             \
+                     dim3(PrefillCfg<DPV>::THREADS), 0, stream, p,                           \
                      static_cast<const uint16_t*>(q), static_cast<const E*>(k),             \
                      static_cast<const E*>(v), static_cast<const E*>(cache), kv_lens,       \
                      page_indices, cu, dist, static_cast<OutS*>(out), plan)
@@ -492,7 +540,7 @@ bool prefill_supported(const Params& p, int q_dtype, int kv_dtype, int out_dtype
   if (out_dtype != RPA_DTYPE_BF16 && out_dtype != RPA_DTYPE_F32) return false;
   if (p.Dp != 128 && p.Dp != 256) return false;
   // 8-element pieces of q / k / v rows; at least one query token per item.
-  if (p.D % 8 != 0 || p.qpk > kRows) return false;
+  if (p.D % 8 != 0 || p.qpk > PrefillCfg<256>::ROWS) return false;
   if (p.S > kMaxDecodeSeqs) return false;
   return true;
 }
