@@ -323,6 +323,16 @@ def test_decode_only_measurement_path(gpu_device):
         run_gpu(p, gpu_device, path=N.RPA_PATH_DECODE_ONLY)
 
 
+@pytest.mark.parametrize("ps,window", [(16, None), (16, 3000), (32, None)])
+def test_prefill_long_context(gpu_device, ps, window):
+    """Prefill chunks whose key range spans more pages than the kernel keeps in
+    LDS (512) read the page table directly; the windowed case starts its range
+    mid-sequence."""
+    check(W.make_workload([(64, 10000), (1, 9000), (200, 16500)], 16, 4, 128, ps, seed=41,
+                          sliding_window=window, distribution=[0, 0, 3], name=f"long-ps{ps}"),
+          gpu_device)
+
+
 @pytest.mark.parametrize("scale", [0.0, -0.05])
 def test_non_positive_sm_scale(gpu_device, scale):
     """sm_scale is a plain multiplier: zero gives uniform attention over the

@@ -140,9 +140,12 @@ int rpa_validate_desc(const rpa_desc* d) {
 
 size_t rpa_workspace_size(const rpa_desc* d) {
   if (rpa_validate_desc(d) != RPA_OK) return 0;
-  const rpa::Params p = make_params(d);
+  rpa::Params p = make_params(d);
   size_t bytes = 256;
-  if (use_decode_kernel(d, p)) bytes += rpa::decode_workspace_bytes(p);
+  if (use_decode_kernel(d, p)) {
+    p.decode_waves = rpa::decode_waves(p, current_num_cus());
+    bytes += rpa::decode_workspace_bytes(p);
+  }
   return bytes;
 }
 

@@ -1,15 +1,16 @@
 // Decode attention (one query token per sequence) for gfx950.
 //
-// Bandwidth-bound GQA split-K.  The key range of every decode sequence is cut
-// into units of up to kMaxTilesPerUnit tiles; the (unit, kv head) items are
-// walked by a persistent grid in grid-stride order (rpa_plan.h), so at any
-// moment the wavefronts of the chip stream the kv heads of a compact window
-// of tokens -- adjacent bytes of the same pages.  A sequence with a single
-// unit writes its output rows directly; otherwise every unit writes an
-// un-normalised partial (m, l, O) to the workspace and the finish kernel
-// (rpa_finish.hip), launched next on the same stream, merges them.  The
-// kernel boundary orders the partial writes before the merge reads, so no
-// wavefront ever waits for another.
+// Bandwidth-bound GQA split-K with a stream-K split (rpa_plan.h): the tiles
+// of every (decode sequence, kv head) pair lie on one line, pair-major, and
+// each wavefront of the persistent grid walks an equal contiguous stretch of
+// it, so every wavefront streams the same number of bytes.  A pair inside one
+// wavefront's stretch gets its output rows directly; a pair cut between
+// wavefronts gets one un-normalised partial (m, l, O) per wavefront, which the
+// finish kernel (rpa_finish.hip), launched next on the same stream, merges.
+// The kernel boundary orders the partial writes before the merge reads, so no
+// wavefront ever waits for another.  Concurrent wavefronts sit at the same
+// offset of consecutive pairs -- the kv heads of the same tokens, adjacent
+// bytes of the same pages.
 //
 // New tokens.  The key at position kv_len - 1 of a decode row is its own new
 // token: unless skip_kv_update, the wavefront that owns the sequence's last
@@ -122,16 +123,16 @@ struct DecodeCfg {
   static_assert(NOCT * NPART == 16, "16 loads per lane per tile");
 };
 
-// One tile of the wavefront's item walk (wavefront-uniform).
+// One tile of the wavefront's walk (wavefront-uniform).
 struct TileInfo {
-  int32_t unit;    // item index: (sequence unit) * Hkv + head; >= total => none
-  int32_t s;       // sequence
-  int32_t h;       // kv head
-  int32_t lt;      // tile index within the sequence
-  int32_t lt_end;  // end tile of the unit
-  int32_t nt;      // tiles of the sequence
-  int32_t lo;      // first key of the sequence's range
-  int32_t hi;      // end of the sequence's range (kv_len)
+  int32_t g;    // position on the work line; >= the stretch's end => none
+  int32_t s;    // sequence
+  int32_t h;    // kv head
+  int32_t lt;   // tile index within the pair
+  int32_t lt0;  // first tile of this wavefront's segment of the pair
+  int32_t nt;   // tiles of the pair
+  int32_t lo;   // first key of the sequence's range
+  int32_t hi;   // end of the sequence's range (kv_len)
 };
 
 __device__ __forceinline__ int32_t uni(int32_t x) { return __builtin_amdgcn_readfirstlane(x); }
@@ -201,7 +202,7 @@ decode_kernel(Params p, const uint16_t* __restrict__ q, const typename KV::stora
               const int32_t* __restrict__ page_indices, const int32_t* __restrict__ cu,
               const int32_t* __restrict__ dist, OutS* __restrict__ out,
               float* __restrict__ part_o, float* __restrict__ part_ml,
-              int32_t* __restrict__ plan_ws, int32_t max_units) {
+              int32_t* __restrict__ plan_ws) {
   using C = DecodeCfg<KV, DP>;
   constexpr int TT = C::TT, NOCT = C::NOCT, NPART = C::NPART, NG = C::NG;
   constexpr int KP = NPART / 2;        // K parts (then V parts)
@@ -220,31 +221,34 @@ decode_kernel(Params p, const uint16_t* __restrict__ q, const typename KV::stora
   const int tl = lane >> 3;  // load shape: token within the octet
   const int ol = lane & 7;   // load shape: 16-byte column within a 128-byte part
 
-  const Plan pl = build_plan(p, kv_lens, cu, dist, TT, max_units, true, L, nullptr);
+  const Plan pl = build_plan(p, kv_lens, cu, dist, TT, true, L, nullptr);
   publish_plan(p, pl, L, cu, plan_ws);
-  const int32_t total_items = pl.total_units * p.Hkv;
   const int32_t gw = static_cast<int32_t>(blockIdx.x) * kWaves + wave;
-  const int32_t nw = static_cast<int32_t>(gridDim.x) * kWaves;
-  if (gw >= total_items) return;  // no barrier follows the plan
+  // This wavefront's stretch [g_begin, g_end) of the work line.
+  const int64_t g_begin64 = static_cast<int64_t>(gw) * pl.tpw;
+  if (g_begin64 >= pl.total_tiles) return;  // no barrier follows the plan
+  const int32_t g_begin = static_cast<int32_t>(g_begin64);
+  const int32_t g_end = min(g_begin + pl.tpw, pl.total_tiles);
   unsigned char* buf = smem + wave * C::WAVE_LDS;
   const int32_t rows = min(p.qpk, 16);
   const int32_t rp = decode_slot_rows(p.qpk);
   const int32_t max_tok = p.pps * p.ps - 1;
   const bool write_kv = p.skip_kv_update == 0;
 
-  // ---- item walk (wavefront-uniform) ---------------------------------------
-  auto locate = [&](int32_t unit) __attribute__((always_inline)) {
+  // ---- walk of the stretch (wavefront-uniform) -----------------------------
+  // Tile g: sequence s with Hkv * base[s] <= g < Hkv * base[s + 1] (the
+  // largest such s is the non-empty one), then head and tile within it.
+  auto locate = [&](int32_t g) __attribute__((always_inline)) {
     TileInfo ti;
-    ti.unit = unit;
-    if (unit >= total_items) return ti;
-    const int32_t pu = unit / p.Hkv;
-    ti.h = uni(unit - pu * p.Hkv);
-    ti.s = uni(find_prefix(L.units, pl.num_seqs, pu));
-    const int32_t u = uni(pu - L.units[ti.s]);
+    ti.g = g;
+    if (g >= g_end) return ti;
+    ti.s = uni(find_prefix(L.base, pl.num_seqs, g / p.Hkv));
     const int32_t dkv = uni(L.dkv[ti.s]);
-    ti.nt = decode_tiles(p, dkv, TT);
-    ti.lt = u * pl.tpu;
-    ti.lt_end = min(ti.nt, ti.lt + pl.tpu);
+    ti.nt = uni(L.base[ti.s + 1] - L.base[ti.s]);
+    const int32_t r = g - p.Hkv * L.base[ti.s];
+    ti.h = uni(r / ti.nt);
+    ti.lt = uni(r - ti.h * ti.nt);
+    ti.lt0 = ti.lt;
     int32_t lo, hi;
     decode_range(p, dkv, &lo, &hi);
     ti.lo = uni(lo);
@@ -252,12 +256,19 @@ decode_kernel(Params p, const uint16_t* __restrict__ q, const typename KV::stora
     return ti;
   };
   auto advance = [&](const TileInfo& c) __attribute__((always_inline)) {
-    if (c.lt + 1 < c.lt_end) {
-      TileInfo ti = c;
+    TileInfo ti = c;
+    ti.g = c.g + 1;
+    if (ti.g >= g_end) return ti;
+    if (c.lt + 1 < c.nt) {
       ti.lt = c.lt + 1;
-      return ti;
+    } else if (c.h + 1 < p.Hkv) {
+      ti.h = c.h + 1;
+      ti.lt = 0;
+      ti.lt0 = 0;
+    } else {
+      ti = locate(ti.g);
     }
-    return locate(c.unit + nw);
+    return ti;
   };
 
   // ---- addressing ------------------------------------------------------------
@@ -308,7 +319,7 @@ decode_kernel(Params p, const uint16_t* __restrict__ q, const typename KV::stora
   };
 
   // ---- pipeline ----------------------------------------------------------------
-  TileInfo cur = locate(gw);
+  TileInfo cur = locate(g_begin);
   uint4 qbuf[2][KK];
   uint4 bufr[2][NOCT][NPART];
   Pages pbuf[2];
@@ -316,7 +327,7 @@ decode_kernel(Params p, const uint16_t* __restrict__ q, const typename KV::stora
   load_tile(cur, pbuf[0], bufr[0]);
   load_q(cur, qbuf[0]);
   TileInfo nxt = advance(cur);
-  pages_of(nxt.unit < total_items ? nxt : cur, pbuf[0]);
+  pages_of(nxt.g < g_end ? nxt : cur, pbuf[0]);
 
   float m_run = -INFINITY;  // per row n, in log2 units
   float l_run = 0.0f;       // this lane's share of the row sum
@@ -332,10 +343,10 @@ decode_kernel(Params p, const uint16_t* __restrict__ q, const typename KV::stora
   // sites, so no register copy forces an early wait on a prefetch.
   auto step = [&](uint4 (*CB)[NPART], uint4 (*NB)[NPART], const uint4* CQ, uint4* NQ,
                   const Pages& CP, Pages& NP) __attribute__((always_inline)) -> bool {
-    const bool has_nxt = nxt.unit < total_items;
+    const bool has_nxt = nxt.g < g_end;
     const TileInfo nn = has_nxt ? advance(nxt) : nxt;
     const TileInfo ldt = has_nxt ? nxt : cur;
-    pages_of(nn.unit < total_items ? nn : ldt, NP);
+    pages_of(nn.g < g_end ? nn : ldt, NP);
     load_tile(ldt, CP, NB);
     load_q(ldt, NQ);
 
@@ -459,14 +470,14 @@ decode_kernel(Params p, const uint16_t* __restrict__ q, const typename KV::stora
       write_new_token<KV, DP>(p, cache, page_indices, keys, values, cur.s, cur.h, cur.hi - 1,
                               tq_cur, lane);
 
-    // ---- end of a unit: finish (single-unit sequence) or write a partial.
-    if (cur.lt + 1 >= cur.lt_end) {
+    // ---- end of this wavefront's segment of a pair: the output (the whole
+    // pair was this wavefront's) or a partial in slot wavefront + pair.
+    if (last_tile || cur.g + 1 >= g_end) {
       float lsum = l_run;
       lsum += __shfl_xor(lsum, 16, 64);
       lsum += __shfl_xor(lsum, 32, 64);
       const int32_t s = cur.s, h = cur.h;
-      const int32_t nunits = L.units[s + 1] - L.units[s];
-      if (nunits == 1) {
+      if (last_tile && cur.lt0 == 0) {
         if (n < rows) {
           const float inv = (lsum == 0.0f) ? 0.0f : p.v_scale / lsum;
           OutS* orow = out + ((static_cast<int64_t>(tq_cur) * p.Hq + h * p.qpk + n) * p.D);
@@ -479,7 +490,7 @@ decode_kernel(Params p, const uint16_t* __restrict__ q, const typename KV::stora
             }
         }
       } else if (n < rows) {
-        const int64_t slot = cur.unit;  // one slot per (unit, head) item
+        const int64_t slot = static_cast<int64_t>(gw) + static_cast<int64_t>(s) * p.Hkv + h;
         float* po = part_o + (slot * rp + n) * DP;
 #pragma unroll
         for (int t = 0; t < NT; ++t)
@@ -515,14 +526,12 @@ hipError_t launch_typed(const Params& p, const DecodeWorkspace& ws, const void* 
     hipLaunchKernelGGL((decode_kernel<KV, DP, OutS, true>), grid, block, 0, stream, p,
                        static_cast<const uint16_t*>(q), static_cast<const E*>(k),
                        static_cast<const E*>(v), static_cast<E*>(cache), kv_lens, page_indices,
-                       cu, dist, static_cast<OutS*>(out), ws.part_o, ws.part_ml, ws.plan,
-                       ws.max_units);
+                       cu, dist, static_cast<OutS*>(out), ws.part_o, ws.part_ml, ws.plan);
   } else {
     hipLaunchKernelGGL((decode_kernel<KV, DP, OutS, false>), grid, block, 0, stream, p,
                        static_cast<const uint16_t*>(q), static_cast<const E*>(k),
                        static_cast<const E*>(v), static_cast<E*>(cache), kv_lens, page_indices,
-                       cu, dist, static_cast<OutS*>(out), ws.part_o, ws.part_ml, ws.plan,
-                       ws.max_units);
+                       cu, dist, static_cast<OutS*>(out), ws.part_o, ws.part_ml, ws.plan);
   }
   return hipGetLastError();
 }
@@ -567,6 +576,9 @@ bool decode_supported(const Params& p, int q_dtype, int kv_dtype, int out_dtype)
   if (p.Dp != 128 && p.Dp != 256) return false;
   if (p.D % 8 != 0 || p.qpk > 16) return false;
   if (p.S > kMaxDecodeSeqs) return false;
+  // The work line (tiles of every pair) is indexed with 32-bit integers.
+  const int64_t tiles = (static_cast<int64_t>(p.pps) * p.ps + 15) / 16;
+  if (static_cast<int64_t>(p.S) * p.Hkv * tiles >= (int64_t(1) << 31)) return false;
   return true;
 }
 
@@ -577,29 +589,17 @@ int decode_waves(const Params& p, int num_cus) {
   return num_cus * kWaves;
 }
 
-// Workspace layout: the partial outputs, one slot per (sequence unit, kv
-// head), then their (m, l) pairs.  Nothing in it needs initialising.
-constexpr size_t kPartialBudget = size_t(256) << 20;
-
-// Capacity in (sequence, unit) pairs.  The device plan grows units whenever
-// the batch would need more.
-static int32_t decode_max_units(const Params& p) {
-  const int64_t rows = decode_slot_rows(p.qpk);
-  const int64_t per_unit = static_cast<int64_t>(p.Hkv) * rows * (p.Dp * 4 + 8);
-  const int64_t unit_tokens = 16;  // smallest tile of any configuration
-  const int64_t need = static_cast<int64_t>(p.S) * ((static_cast<int64_t>(p.pps) * p.ps + unit_tokens - 1) / unit_tokens);
-  int64_t cap = static_cast<int64_t>(kPartialBudget) / per_unit;
-  if (cap < p.S + 1024) cap = p.S + 1024;
-  int64_t m = need < cap ? need : cap;
-  if (m < p.S + 1) m = p.S + 1;
-  return static_cast<int32_t>(m);
+// Partial slots: one per (wavefront, pair) segment, indexed wavefront +
+// pair (rpa_plan.h), so decode_waves + max_num_seqs * Hkv bound them.
+static int64_t decode_slots(const Params& p) {
+  return static_cast<int64_t>(p.decode_waves) + static_cast<int64_t>(p.S) * p.Hkv;
 }
 
 // Workspace layout: the partials, then the published plan.  Nothing in it
 // needs initialising.
 size_t decode_workspace_bytes(const Params& p) {
   const int64_t rows = decode_slot_rows(p.qpk);
-  const int64_t slots = static_cast<int64_t>(decode_max_units(p)) * p.Hkv;
+  const int64_t slots = decode_slots(p);
   size_t bytes = 256;
   bytes += static_cast<size_t>(slots) * rows * p.Dp * sizeof(float);  // part_o
   bytes += static_cast<size_t>(slots) * rows * 2 * sizeof(float);     // part_ml
@@ -610,13 +610,12 @@ size_t decode_workspace_bytes(const Params& p) {
 DecodeWorkspace carve_decode_workspace(const Params& p, void* base) {
   DecodeWorkspace ws;
   const int64_t rows = decode_slot_rows(p.qpk);
-  ws.max_units = decode_max_units(p);
-  const int64_t slots = static_cast<int64_t>(ws.max_units) * p.Hkv;
+  ws.slots = decode_slots(p);
   uintptr_t ptr = (reinterpret_cast<uintptr_t>(base) + 255) & ~static_cast<uintptr_t>(255);
   ws.part_o = reinterpret_cast<float*>(ptr);
-  ptr += static_cast<size_t>(slots) * rows * p.Dp * sizeof(float);
+  ptr += static_cast<size_t>(ws.slots) * rows * p.Dp * sizeof(float);
   ws.part_ml = reinterpret_cast<float*>(ptr);
-  ptr += static_cast<size_t>(slots) * rows * 2 * sizeof(float);
+  ptr += static_cast<size_t>(ws.slots) * rows * 2 * sizeof(float);
   ws.plan = reinterpret_cast<int32_t*>(ptr);
   return ws;
 }

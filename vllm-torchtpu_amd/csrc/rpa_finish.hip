@@ -3,11 +3,11 @@
 // Launched right after the decode kernel on the same stream (or alone, when
 // the decode kernel does not apply).  A persistent grid walks three kinds of
 // items in grid-stride order:
-//   merge   (decode sequence s, kv head h) with more than one unit: combine
-//           the unit partials (m, l, O) the decode kernel wrote -- the
-//           split-K form of the online softmax, out = sum_k 2^(m_k - M) O_k /
-//           sum_k 2^(m_k - M) l_k * v_scale.  The kernel boundary makes the
-//           partials visible; nothing waits on another wavefront.
+//   merge   (decode sequence s, kv head h) cut between several decode
+//           wavefronts (rpa_plan.h): combine their partials (m, l, O) --
+//           the split-K form of the online softmax, out = sum_k 2^(m_k - M)
+//           O_k / sum_k 2^(m_k - M) l_k * v_scale.  The kernel boundary makes
+//           the partials visible; nothing waits on another wavefront.
 //   write   token row t of a non-decode sequence: its new K/V record into
 //           its cache page (kernel.py:154-166), unless skip_kv_update.
 //   attend  (token row t, q head g) of a non-decode sequence: generic_row
@@ -37,7 +37,7 @@ finish_kernel(Params p, const uint16_t* __restrict__ q, const typename KVT::stor
               const int32_t* __restrict__ page_indices, const int32_t* __restrict__ cu,
               const int32_t* __restrict__ dist, OutS* __restrict__ out,
               const float* __restrict__ part_o, const float* __restrict__ part_ml,
-              const int32_t* __restrict__ plan, int32_t max_units) {
+              const int32_t* __restrict__ plan) {
   using E = typename KVT::storage;
   __shared__ PlanCore L;
   __shared__ PlanRows R;
@@ -53,10 +53,10 @@ finish_kernel(Params p, const uint16_t* __restrict__ q, const typename KVT::stor
   if (decode_on) {
     n = min(max(pv.hdr[0], 0), p.S);
   } else {
-    n = build_plan(p, kv_lens, cu, dist, decode_tile_tokens(DP, sizeof(E)), max_units, false, L, &R)
-            .num_seqs;
+    n = build_plan(p, kv_lens, cu, dist, decode_tile_tokens(DP, sizeof(E)), false, L, &R).num_seqs;
   }
   const int32_t nmerge = decode_on ? n * p.Hkv : 0;
+  const int32_t tpw = decode_on ? max(pv.hdr[1], 1) : 1;
   const int32_t nwrite = p.skip_kv_update ? 0 : p.T;
   const int64_t nattend = p.prefill_on ? 0 : static_cast<int64_t>(p.T) * p.Hq;
   const int64_t total = static_cast<int64_t>(nmerge) + nwrite + nattend;
@@ -70,17 +70,22 @@ finish_kernel(Params p, const uint16_t* __restrict__ q, const typename KVT::stor
     if (it < nmerge) {
       const int32_t s = static_cast<int32_t>(it / p.Hkv);
       const int32_t h = static_cast<int32_t>(it - static_cast<int64_t>(s) * p.Hkv);
-      const int32_t u0 = pv.units[s];
-      const int32_t nunits = pv.units[s + 1] - u0;
-      if (pv.dkv[s] == 0 || nunits <= 1) continue;
-      const int32_t first = u0 * p.Hkv + h;
+      // The pair's tiles [g0, g0 + nt) of the work line; the wavefronts
+      // owning its first and last tile, and its partial slots w + pair.
+      const int32_t nt = pv.base[s + 1] - pv.base[s];
+      if (pv.dkv[s] == 0 || nt <= 0) continue;
+      const int32_t g0 = p.Hkv * pv.base[s] + h * nt;
+      const int32_t wa = g0 / tpw, wb = (g0 + nt - 1) / tpw;
+      if (wa == wb) continue;  // one wavefront finished the pair
+      const int32_t first = wa + static_cast<int32_t>(it);
+      const int32_t nparts = wb - wa + 1;
       const int64_t orow0 = static_cast<int64_t>(pv.tq[s]) * p.Hq + h * p.qpk;
       switch (rp) {
-        case 1: merge_partials<DP, 1, false>(p, part_o, part_ml, first, nunits, rows, out, orow0); break;
-        case 2: merge_partials<DP, 2, false>(p, part_o, part_ml, first, nunits, rows, out, orow0); break;
-        case 4: merge_partials<DP, 4, false>(p, part_o, part_ml, first, nunits, rows, out, orow0); break;
-        case 8: merge_partials<DP, 8, false>(p, part_o, part_ml, first, nunits, rows, out, orow0); break;
-        default: merge_partials<DP, 16, false>(p, part_o, part_ml, first, nunits, rows, out, orow0); break;
+        case 1: merge_partials<DP, 1>(p, part_o, part_ml, first, nparts, rows, out, orow0); break;
+        case 2: merge_partials<DP, 2>(p, part_o, part_ml, first, nparts, rows, out, orow0); break;
+        case 4: merge_partials<DP, 4>(p, part_o, part_ml, first, nparts, rows, out, orow0); break;
+        case 8: merge_partials<DP, 8>(p, part_o, part_ml, first, nparts, rows, out, orow0); break;
+        default: merge_partials<DP, 16>(p, part_o, part_ml, first, nparts, rows, out, orow0); break;
       }
       continue;
     }
@@ -130,7 +135,7 @@ hipError_t launch_dp(const Params& p, const DecodeWorkspace& ws, const void* q, 
   hipLaunchKernelGGL((finish_kernel<KVT, DPV, OutS>), grid, block, 0, stream, p,                  \
                      static_cast<const uint16_t*>(q), static_cast<const E*>(k),                   \
                      static_cast<const E*>(v), static_cast<E*>(cache), kv_lens, page_indices, cu, \
-                     dist, static_cast<OutS*>(out), ws.part_o, ws.part_ml, ws.plan, ws.max_units)
+                     dist, static_cast<OutS*>(out), ws.part_o, ws.part_ml, ws.plan)
   if (p.Dp == 128) {
     RPA_FINISH_LAUNCH(128);
   } else if (p.Dp == 256) {

@@ -20,21 +20,22 @@ constexpr int kMaxDecodeSeqs = 2048;
 // Slices of the caller's workspace used by the decode path (no
 // initialisation needed).
 struct DecodeWorkspace {
-  float* part_o;      // [max_units * Hkv][rows][Dp] un-normalised partial outputs
-  float* part_ml;     // [max_units * Hkv][rows][2] (row max in log2 units, row sum)
-  int32_t* plan;      // the decode kernel's plan for the finish kernel (layout below)
-  int32_t max_units;  // capacity in (sequence, unit) pairs
+  float* part_o;   // [slots][rows][Dp] un-normalised partial outputs
+  float* part_ml;  // [slots][rows][2] (row max in log2 units, row sum)
+  int32_t* plan;   // the decode kernel's plan for the finish kernel (layout below)
+  int64_t slots;   // decode wavefronts + max_num_seqs * Hkv (the stream-K slot bound)
 };
 
 
-// Plan written by the decode kernel: [0] num_seqs n, [1] tiles per unit,
-// [2] total units, [3] sequences with non-decode rows; units[S + 1] (exclusive prefix, units[n] =
-// total), dkv[S] (kv_len of a decode sequence, else 0), tq[S] (q row of the
+// Plan written by the decode kernel (rpa_plan.h): [0] num_seqs n, [1] tiles
+// per wavefront, [2] total tiles G, [3] sequences with non-decode rows;
+// base[S + 1] (exclusive prefix of tiles per sequence, base[n] = total),
+// dkv[S] (kv_len of a decode sequence, else 0), tq[S] (q row of the
 // sequence), rowseq[T] (sequence of a token row the finish kernel owns, -1 for
 // decode rows and padding rows).
 struct PlanView {
   const int32_t* hdr;
-  const int32_t* units;
+  const int32_t* base;
   const int32_t* dkv;
   const int32_t* tq;
   const int32_t* rowseq;
@@ -42,8 +43,8 @@ struct PlanView {
 __host__ __device__ inline PlanView plan_view(const int32_t* plan, int32_t S) {
   PlanView v;
   v.hdr = plan;
-  v.units = plan + 4;
-  v.dkv = v.units + (S + 1);
+  v.base = plan + 4;
+  v.dkv = v.base + (S + 1);
   v.tq = v.dkv + S;
   v.rowseq = v.tq + S;
   return v;
@@ -57,8 +58,9 @@ int decode_waves(const Params& p, int num_cus);
 size_t decode_workspace_bytes(const Params& p);
 DecodeWorkspace carve_decode_workspace(const Params& p, void* base);
 
-// Decode rows: balanced split-K MFMA decode; writes single-unit outputs and
-// partials, and the decode rows' new tokens into the cache.
+// Decode rows: stream-K split MFMA decode; writes the outputs of pairs one
+// wavefront finishes and partials of the others, and the decode rows' new
+// tokens into the cache.
 hipError_t launch_decode(const Params& p, int kv_dtype, int out_dtype, const DecodeWorkspace& ws,
                          const void* q, const void* k, const void* v, void* cache,
                          const int32_t* kv_lens, const int32_t* page_indices, const int32_t* cu,

@@ -1,24 +1,19 @@
-// Split-K merge of decode partials, shared by the decode kernel (which merges
-// in-launch, reading other wavefronts' partials with coherent loads) and the
-// finish kernel (which merges after the kernel boundary).
+// Split-K merge of decode partials (the finish kernel's merge items).
 //
-// Each unit k of a (sequence, kv head) left (m_k, l_k, O_k): row max of its
-// scores (log2 units), row sum of 2^(s - m_k), and sum of 2^(s - m_k) v.  The
-// merged row is out = sum_k 2^(m_k - M) O_k / sum_k 2^(m_k - M) l_k * v_scale
-// with M = max_k m_k -- the online-softmax recurrence of kernel.py:486-557
-// applied across units.
+// Each wavefront k that touched a (sequence, kv head) pair left (m_k, l_k, O_k):
+// row max of its scores (log2 units), row sum of 2^(s - m_k), and sum of
+// 2^(s - m_k) v.  The merged row is out = sum_k 2^(m_k - M) O_k /
+// sum_k 2^(m_k - M) l_k * v_scale with M = max_k m_k -- the online-softmax
+// recurrence of kernel.py:486-557 applied across key ranges.  The partials
+// were written by the previous launch, so plain loads see them.
 #pragma once
 
 #include "rpa_common.h"
 
 namespace rpa {
 
-// Cache policy of a coherent load: sc1 (system-coherent), so the load misses
-// any stale copy in this XCD's L2.
-constexpr int kCoherentLoad = 16;
-
 // Merge the `nunits` partials of one (sequence, kv head) and write its output
-// rows [0, rows).  The partial of unit k sits in slot first + k * Hkv: RP rows
+// rows [0, rows).  Partial k sits in slot first + k: RP rows
 // x DP floats of un-normalised O, and RP (m, l) pairs (log2 units).  One
 // wavefront; lane e of load j covers element e + 64 j of a slot, so every
 // load is a wave-wide contiguous 256-byte read and row (j * 64 / DP) is the
@@ -33,9 +28,7 @@ __device__ __forceinline__ void ml_combine(float& M, float& L, float m, float l)
   M = mn;
 }
 
-// COHERENT: partials written by other wavefronts of the same launch, read with
-// relaxed agent-scope atomic loads (coherent across XCDs).
-template <int DP, int RP, bool COHERENT, typename OutS>
+template <int DP, int RP, typename OutS>
 __device__ __forceinline__ void merge_partials(const Params& p, const float* __restrict__ part_o,
                                                const float* __restrict__ part_ml, int32_t first,
                                                int32_t nunits, int32_t rows,
@@ -43,33 +36,12 @@ __device__ __forceinline__ void merge_partials(const Params& p, const float* __r
   constexpr int NDW = RP * DP / 64;  // dwords per lane per slot
   constexpr int UB = NDW >= 64 ? 1 : (64 / NDW > 16 ? 16 : 64 / NDW);  // units per batch
   const int lane = threadIdx.x & 63;
-  const int64_t stride = static_cast<int64_t>(p.Hkv);
   // Element offsets of unit k's O row block (this lane's first element) and of
   // its (m, l) pairs.
-  auto off_o = [&](int32_t k) { return (first + k * stride) * (RP * DP) + lane; };
-  auto off_ml = [&](int32_t k) { return (first + k * stride) * (2 * RP); };
-  // Coherent loads are buffer loads with the sc1 policy (they see other XCDs'
-  // completed write-through stores); the partial region is far below 2 GiB.
-  const __amdgpu_buffer_rsrc_t ro =
-      __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(part_o), 0, 0x7fffffff, 0x00020000);
-  const __amdgpu_buffer_rsrc_t rm =
-      __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(part_ml), 0, 0x7fffffff, 0x00020000);
-  auto ld_o = [&](int64_t e) __attribute__((always_inline)) -> float {
-    if constexpr (COHERENT) {
-      return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
-                                           ro, static_cast<int32_t>(e * 4), 0, kCoherentLoad));
-    } else {
-      return part_o[e];
-    }
-  };
-  auto ld_ml = [&](int64_t e) __attribute__((always_inline)) -> float {
-    if constexpr (COHERENT) {
-      return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
-                                           rm, static_cast<int32_t>(e * 4), 0, kCoherentLoad));
-    } else {
-      return part_ml[e];
-    }
-  };
+  auto off_o = [&](int32_t k) { return (static_cast<int64_t>(first) + k) * (RP * DP) + lane; };
+  auto off_ml = [&](int32_t k) { return (static_cast<int64_t>(first) + k) * (2 * RP); };
+  auto ld_o = [&](int64_t e) __attribute__((always_inline)) -> float { return part_o[e]; };
+  auto ld_ml = [&](int64_t e) __attribute__((always_inline)) -> float { return part_ml[e]; };
 
   // Issue the (m, l) pairs of unit `lane` and the first batch of O rows.
   float2 ml0[RP];

@@ -9,12 +9,22 @@
 //                    history, or the last W keys under a causal window
 //                    (kernel.py:196-204 with p = kv_len - 1).
 //   tile             TT consecutive keys of one sequence (one kv head).
-//   unit             up to `tpu` consecutive tiles of one decode sequence;
-//                    units of all sequences are numbered in sequence order.
-//   item             (unit, kv head) = unit * Hkv + h: the decode kernel's
-//                    work granule, walked in grid-stride order so that
-//                    concurrent wavefronts read the kv heads of the same
-//                    tokens (adjacent bytes of a page).
+//   pair             (decode sequence s, kv head h), numbered p = s * Hkv + h.
+//   work order       every tile of every pair on one line, pair-major:
+//                    g = Hkv * base[s] + h * nt_s + t for tile t of pair
+//                    (s, h), with nt_s the sequence's tiles and base[s] their
+//                    exclusive prefix.
+//   stream-K split   wavefront w of the decode kernel's persistent grid walks
+//                    tiles [w * tpw, (w + 1) * tpw) of that line, tpw =
+//                    cdiv(G, W) for G tiles and W wavefronts: every wavefront
+//                    gets the same number of tiles.  A pair that lies inside
+//                    one wavefront's range is finished there; a pair cut by
+//                    range ends leaves one partial per wavefront that touched
+//                    it, in slot w + p.  Slots never collide: wavefronts and
+//                    pairs are both ordered intervals of the line, so
+//                    w1 < w2 with both touching pairs p1, p2 forces p1 <= p2.
+//                    The partials of pair p are slots w_a + p .. w_b + p with
+//                    w_a, w_b the wavefronts owning its first and last tile.
 #pragma once
 
 #include "rpa_common.h"
@@ -27,8 +37,8 @@ constexpr int kPlanWaves = kPlanThreads / 64;
 
 struct Plan {
   int32_t num_seqs;     // min(distribution[2], S)
-  int32_t tpu;          // tiles per unit
-  int32_t total_units;  // (sequence, unit) pairs over all decode sequences
+  int32_t tpw;          // tiles per wavefront (>= 1)
+  int32_t total_tiles;  // G: tiles of all pairs
   int32_t n_other;      // sequences with rows that are not decode rows
   int32_t cu_end;       // cu_q_lens[num_seqs]
 };
@@ -39,7 +49,7 @@ struct Plan {
 template <int N>
 struct PlanCoreT {
   static constexpr int kCap = N;  // sequences the plan holds
-  int32_t units[N + 1];  // exclusive prefix of units; units[n] = total
+  int32_t base[N + 1];   // exclusive prefix of tiles per sequence; base[n] = total
   int32_t dkv[N];        // kv_len of a decode sequence (clamped), else 0
   int32_t tq[N];         // q row of the sequence (cu_q_lens[s], clamped)
   int32_t red[3 * kPlanWaves];
@@ -91,22 +101,6 @@ __device__ __forceinline__ void block_exclusive_scan(int32_t* a, int32_t n, int3
   __syncthreads();
 }
 
-// Tiles per unit: about four items per decode wavefront (so the grid-stride
-// walk ends evenly), at most kMaxTilesPerUnit (a unit's partial is a few KiB
-// against 100+ KiB of keys), and at least what the partial-slot capacity
-// (max_units) requires.
-constexpr int kMaxTilesPerUnit = 8;
-
-__device__ __forceinline__ int32_t plan_tiles_per_unit(int64_t total_tiles, int32_t nseq,
-                                                       int32_t hkv, int32_t decode_waves,
-                                                       int32_t max_units) {
-  int64_t tpu = (total_tiles * hkv) / (4 * static_cast<int64_t>(max(decode_waves, 1)));
-  tpu = tpu < 1 ? 1 : (tpu > kMaxTilesPerUnit ? kMaxTilesPerUnit : tpu);
-  const int64_t budget = max<int64_t>(1, static_cast<int64_t>(max_units) - nseq);
-  const int64_t need = (total_tiles + budget - 1) / budget;
-  return static_cast<int32_t>(tpu > need ? tpu : need);
-}
-
 // Tiles of a decode sequence with kv_len dkv (0 for a non-decode sequence).
 __device__ __forceinline__ int32_t decode_tiles(const Params& p, int32_t dkv, int32_t tile) {
   if (dkv <= 0) return 0;
@@ -122,8 +116,7 @@ __device__ __forceinline__ int32_t decode_tiles(const Params& p, int32_t dkv, in
 template <typename PlanLds>
 __device__ __forceinline__ Plan build_plan(const Params& p, const int32_t* kv_lens,
                                            const int32_t* cu, const int32_t* dist, int32_t tile,
-                                           int32_t max_units, bool decode_enabled, PlanLds& L,
-                                           PlanRows* R) {
+                                           bool decode_enabled, PlanLds& L, PlanRows* R) {
   Plan pl;
   const int tid = threadIdx.x;
   const int32_t n = min(num_seqs_of(dist, p.S), PlanLds::kCap);
@@ -137,7 +130,7 @@ __device__ __forceinline__ Plan build_plan(const Params& p, const int32_t* kv_le
     others += (!dec && cu[s + 1] > cu[s]) ? 1 : 0;
     L.dkv[s] = dec ? kl : 0;
     L.tq[s] = min(max(cu[s], 0), max(p.T - 1, 0));
-    L.units[s] = nt;  // tiles for now; turned into units below
+    L.base[s] = nt;  // scanned into the prefix below
     if (R != nullptr) {
       R->kvlen[s] = kl;
       R->cu[s] = cu[s];
@@ -165,12 +158,13 @@ __device__ __forceinline__ Plan build_plan(const Params& p, const int32_t* kv_le
   }
   pl.n_other = nother;
   pl.cu_end = cu[n];
+  (void)nseq;
   __syncthreads();
-  pl.tpu = plan_tiles_per_unit(total_tiles, nseq, p.Hkv, p.decode_waves, max_units);
-  for (int32_t s = tid; s < n; s += kPlanThreads) L.units[s] = (L.units[s] + pl.tpu - 1) / pl.tpu;
-  __syncthreads();
-  block_exclusive_scan(L.units, n, L.red);
-  pl.total_units = L.units[n];
+  block_exclusive_scan(L.base, n, L.red);
+  const int64_t g = total_tiles * p.Hkv;
+  pl.total_tiles = static_cast<int32_t>(g);
+  const int64_t w = max(p.decode_waves, 1);
+  pl.tpw = static_cast<int32_t>(max<int64_t>(1, (g + w - 1) / w));
   return pl;
 }
 
@@ -180,7 +174,7 @@ template <typename PlanLds>
 __device__ __forceinline__ void publish_plan(const Params& p, const Plan& pl, const PlanLds& L,
                                              const int32_t* cu, int32_t* plan) {
   const PlanView v = plan_view(plan, p.S);
-  int32_t* units = const_cast<int32_t*>(v.units);
+  int32_t* base = const_cast<int32_t*>(v.base);
   int32_t* dkv = const_cast<int32_t*>(v.dkv);
   int32_t* tq = const_cast<int32_t*>(v.tq);
   int32_t* rowseq = const_cast<int32_t*>(v.rowseq);
@@ -189,11 +183,11 @@ __device__ __forceinline__ void publish_plan(const Params& p, const Plan& pl, co
   if (blockIdx.x == 0) {
     if (tid == 0) {
       plan[0] = n;
-      plan[1] = pl.tpu;
-      plan[2] = pl.total_units;
+      plan[1] = pl.tpw;
+      plan[2] = pl.total_tiles;
       plan[3] = pl.n_other;
     }
-    for (int32_t s = tid; s <= n; s += kPlanThreads) units[s] = L.units[s];
+    for (int32_t s = tid; s <= n; s += kPlanThreads) base[s] = L.base[s];
     for (int32_t s = tid; s < n; s += kPlanThreads) {
       dkv[s] = L.dkv[s];
       tq[s] = L.tq[s];

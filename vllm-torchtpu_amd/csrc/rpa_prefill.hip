@@ -85,8 +85,14 @@ struct PrefillCfg {
   static constexpr int ROWS = 32 * THREADS / 64;   // q rows per item (32 per wavefront)
   static constexpr int BK = DP == 128 ? 64 : 32;   // keys per tile
   static constexpr int NSB = BK / 32;              // 32-key S^T blocks per tile
-  static constexpr int KS = 2 * DP + 16;           // LDS K row stride (bytes)
-  static constexpr int VS = 2 * DP + 32;           // LDS V row stride (bytes)
+  // LDS row strides.  K rows (read 16 bytes per lane, 16 consecutive keys
+  // per access) are padded by 16 bytes, 4 banks apart; V rows (read with
+  // ds_read_b64_tr_b16: 4 keys x 32 bytes per 16-lane group, two groups 32
+  // bytes apart per access) by 64 bytes, which puts the 4 keys 16 banks
+  // apart so both groups' 8 rows of 8 banks are disjoint.  A 32-byte pad
+  // makes those reads 2-way conflicted.
+  static constexpr int KS = 2 * DP + 16;
+  static constexpr int VS = 2 * DP + 64;
   static constexpr int BUF = BK * (KS + VS);       // one K|V tile buffer
   static constexpr int PPK = 2 * DP / 8;           // 8-element pieces per key (K then V)
   static constexpr int KPI = THREADS / PPK;        // keys covered per staging step
@@ -100,7 +106,7 @@ struct PrefillCfg {
 
 // Page ids of an item's key range kept in LDS (longer ranges read the page
 // table directly).
-constexpr int kItemPages = 1024;
+constexpr int kItemPages = 512;
 // Lazy rescaling: a row's reference max moves only when a tile's max exceeds
 // it by more than 2^kRescaleLog2 (P values then stay below 2^8).
 constexpr float kRescaleLog2 = 8.0f;
