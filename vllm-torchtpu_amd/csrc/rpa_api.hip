@@ -206,12 +206,14 @@ int rpa_forward(const rpa_desc* d, const void* queries, const void* keys, const 
     if (e != hipSuccess) return RPA_ERR_LAUNCH;
     if (decode_only) return RPA_OK;
   }
+  // The prefill launch also carries the merge and write items; the finish
+  // kernel runs only for shapes the prefill kernel does not take.
   if (rpa::prefill_supported(p, d->q_dtype, d->kv_dtype, d->out_dtype)) {
+    p.prefill_on = 1;
     hipError_t e = rpa::launch_prefill(p, d->kv_dtype, d->out_dtype, queries, keys, values,
                                        kv_cache, kv_lens, page_indices, cu_q_lens, distribution,
-                                       out, ws.plan, s);
-    if (e != hipSuccess) return RPA_ERR_LAUNCH;
-    p.prefill_on = 1;
+                                       out, ws, cus, s);
+    return e == hipSuccess ? RPA_OK : RPA_ERR_LAUNCH;
   }
   hipError_t e = rpa::launch_finish(p, d->kv_dtype, d->out_dtype, ws, queries, keys, values,
                                     kv_cache, kv_lens, page_indices, cu_q_lens, distribution, out,

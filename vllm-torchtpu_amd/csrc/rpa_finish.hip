@@ -17,9 +17,9 @@
 // Every workgroup first derives the decode kernel's plan (rpa_plan.h) from
 // the device-resident metadata.
 #include "rpa_common.h"
+#include "rpa_finish_items.h"
 #include "rpa_generic_row.h"
 #include "rpa_internal.h"
-#include "rpa_merge.h"
 #include "rpa_plan.h"
 
 namespace rpa {
@@ -56,71 +56,34 @@ finish_kernel(Params p, const uint16_t* __restrict__ q, const typename KVT::stor
     n = build_plan(p, kv_lens, cu, dist, decode_tile_tokens(DP, sizeof(E)), false, L, &R).num_seqs;
   }
   const int32_t nmerge = decode_on ? n * p.Hkv : 0;
-  const int32_t tpw = decode_on ? max(pv.hdr[1], 1) : 1;
   const int32_t nwrite = p.skip_kv_update ? 0 : p.T;
   const int64_t nattend = p.prefill_on ? 0 : static_cast<int64_t>(p.T) * p.Hq;
   const int64_t total = static_cast<int64_t>(nmerge) + nwrite + nattend;
-  const int32_t rows = min(p.qpk, 16);
-  const int32_t rp = decode_slot_rows(p.qpk);
-  const int32_t kv_cap = p.pps * p.ps;
 
   const int64_t gw = static_cast<int64_t>(blockIdx.x) * kWaves + wave;
   const int64_t nw = static_cast<int64_t>(gridDim.x) * kWaves;
   for (int64_t it = gw; it < total; it += nw) {
     if (it < nmerge) {
-      const int32_t s = static_cast<int32_t>(it / p.Hkv);
-      const int32_t h = static_cast<int32_t>(it - static_cast<int64_t>(s) * p.Hkv);
-      // The pair's tiles [g0, g0 + nt) of the work line; the wavefronts
-      // owning its first and last tile, and its partial slots w + pair.
-      const int32_t nt = pv.base[s + 1] - pv.base[s];
-      if (pv.dkv[s] == 0 || nt <= 0) continue;
-      const int32_t g0 = p.Hkv * pv.base[s] + h * nt;
-      const int32_t wa = g0 / tpw, wb = (g0 + nt - 1) / tpw;
-      if (wa == wb) continue;  // one wavefront finished the pair
-      const int32_t first = wa + static_cast<int32_t>(it);
-      const int32_t nparts = wb - wa + 1;
-      const int64_t orow0 = static_cast<int64_t>(pv.tq[s]) * p.Hq + h * p.qpk;
-      switch (rp) {
-        case 1: merge_partials<DP, 1>(p, part_o, part_ml, first, nparts, rows, out, orow0); break;
-        case 2: merge_partials<DP, 2>(p, part_o, part_ml, first, nparts, rows, out, orow0); break;
-        case 4: merge_partials<DP, 4>(p, part_o, part_ml, first, nparts, rows, out, orow0); break;
-        case 8: merge_partials<DP, 8>(p, part_o, part_ml, first, nparts, rows, out, orow0); break;
-        default: merge_partials<DP, 16>(p, part_o, part_ml, first, nparts, rows, out, orow0); break;
-      }
+      finish_merge_item<DP, OutS>(p, pv, static_cast<int32_t>(it), part_o, part_ml, out);
       continue;
     }
-    // Row items: the sequence of token row t (-1: not this kernel's row).
-    const bool is_write = it < static_cast<int64_t>(nmerge) + nwrite;
-    const int64_t a = it - nmerge - (is_write ? 0 : nwrite);
-    const int32_t t = static_cast<int32_t>(is_write ? a : a / p.Hq);
-    int32_t s, q_start, q_end, kv_len;
-    if (decode_on) {
-      s = pv.rowseq[t];
-      if (s < 0 || s >= n) continue;
-      q_start = cu[s];
-      q_end = cu[s + 1];
-      kv_len = min(kv_lens[s], kv_cap);
-    } else {
-      s = find_seq(R.cu, n + 1, t);
-      if (s < 0 || s >= n) continue;
-      q_start = R.cu[s];
-      q_end = R.cu[s + 1];
-      kv_len = R.kvlen[s];
-    }
-    if (t < q_start || t >= q_end) continue;
-    const int32_t q_len = q_end - q_start;
-    if (is_write) {
-      const int32_t j = kv_len - q_len + (t - q_start);
-      if (j >= 0) write_record<E>(p, cache, page_indices, keys, values, s, j, t, lane);
+    if (it < static_cast<int64_t>(nmerge) + nwrite) {
+      finish_write_item<E>(p, decode_on, pv, &R, n, cu, kv_lens, cache, page_indices, keys,
+                           values, static_cast<int32_t>(it - nmerge), lane);
       continue;
     }
+    // Attend item (token row t, q head g).
+    const int64_t a = it - nmerge - nwrite;
+    const int32_t t = static_cast<int32_t>(a / p.Hq);
     const int32_t g = static_cast<int32_t>(a - static_cast<int64_t>(t) * p.Hq);
+    RowOwner o;
+    if (!row_owner(p, decode_on, pv, &R, n, cu, kv_lens, t, &o)) continue;
     wave_lds_sync();  // the previous item's reads of qs are complete
     const uint16_t* qrow = q + (static_cast<int64_t>(t) * p.Hq + g) * p.D;
     for (int d = lane; d < DP; d += 64) qs[wave][d] = d < p.D ? bf16_bits_to_f32(qrow[d]) : 0.0f;
     wave_lds_sync();
     generic_row<KVT, OutS>(p, qs[wave], cache, keys, values, p.skip_kv_update == 0, page_indices,
-                           s, t, g, q_start, q_len, kv_len, out);
+                           o.s, t, g, o.q_start, o.q_end - o.q_start, o.kv_len, out);
   }
 }
 

@@ -67,15 +67,20 @@ hipError_t launch_decode(const Params& p, int kv_dtype, int out_dtype, const Dec
                          const int32_t* dist, void* out, hipStream_t stream);
 
 // Prefill kernel: MFMA attention of every row the decode kernel does not
-// take (new tokens read from k/v; their cache write is the finish kernel's).
+// take (new tokens read from k/v), plus, in finish workgroups appended to its
+// grid, the finish kernel's merge and write items (the finish kernel is then
+// not launched).
 bool prefill_supported(const Params& p, int q_dtype, int kv_dtype, int out_dtype);
-// With the decode kernel on (p.decode_waves > 0) `plan` is its published
-// plan, and a batch without non-decode rows ends the launch at once.
+int prefill_merge_blocks(const Params& p, int num_cus);
+int prefill_write_blocks(const Params& p, int num_cus);
+// With the decode kernel on (p.decode_waves > 0) `ws` holds its partials and
+// published plan, and a batch without non-decode rows ends the attention
+// blocks at once.
 hipError_t launch_prefill(const Params& p, int kv_dtype, int out_dtype, const void* q,
-                          const void* k, const void* v, const void* cache,
-                          const int32_t* kv_lens, const int32_t* page_indices,
-                          const int32_t* cu, const int32_t* dist, void* out,
-                          const int32_t* plan, hipStream_t stream);
+                          const void* k, const void* v, void* cache, const int32_t* kv_lens,
+                          const int32_t* page_indices, const int32_t* cu, const int32_t* dist,
+                          void* out, const DecodeWorkspace& ws, int num_cus,
+                          hipStream_t stream);
 
 // Finish kernel: merges the decode partials, writes the new tokens of every
 // non-decode row into the cache and, unless p.prefill_on, attends those rows

@@ -20,6 +20,13 @@
 // {0-3, 8-11} (c = 0) and {4-7, 12-15} (c = 1), and the V^T operand is read
 // with the same key permutation (two 4-key transposing reads per k-step).
 //
+// Extra workgroups do the work that follows the decode kernel
+// (rpa_finish_items.h), independent of the attention blocks (which read new
+// tokens from the k/v inputs, never from the pages being written): the first
+// `nfm` workgroups merge the decode partials (short, latency-bound: dispatched
+// first), the last `nfw` write the new K/V records of the non-decode rows
+// into their pages (bandwidth filler for the tail of the launch).
+//
 // Semantics (ref_ragged_paged_attention, kernel.py:185-209): row i of
 // sequence s sits at position p = kv_len - q_len + i; keys j <= p (and
 // j > p - W under a window) with s_j = q . k_j * sm_scale * k_scale * q_scale,
@@ -29,6 +36,7 @@
 // after this one, writes them into their pages.  P is rounded to bf16 for
 // the PV product (kernel.py:553); everything else accumulates in fp32.
 #include "rpa_common.h"
+#include "rpa_finish_items.h"
 #include "rpa_internal.h"
 #include "rpa_plan.h"
 
@@ -102,6 +110,7 @@ struct PrefillCfg {
   static_assert(THREADS % PPK == 0 && BK % KPI == 0, "whole pieces per thread");
   static_assert(THREADS >= kPlanThreads && 3 * kPlanWaves >= THREADS / 64, "plan scan fits");
   static_assert(2 * BUF >= 4 * (kMaxDecodeSeqs + 1), "plan scratch fits the tile buffers");
+  static_assert(2 * BUF >= sizeof(PlanCore) + sizeof(PlanRows), "finish plan fits the tile buffers");
 };
 
 // Page ids of an item's key range kept in LDS (longer ranges read the page
@@ -123,6 +132,41 @@ __device__ __forceinline__ int32_t prefill_blocks(const Params& p, const int32_t
   return (q_len + bq - 1) / bq;
 }
 
+// Finish workgroup `fb` of `nfin` (pw wavefronts each) walks the merge items
+// (merges) or the write items (!merges) of rpa_finish_items.h, grid-stride
+// over the group's wavefronts.  `smem` (the tile buffers, unused here) holds
+// the plan when the decode kernel did not publish one.
+template <typename E, int DP, typename OutS>
+__device__ __forceinline__ void prefill_finish_role(
+    const Params& p, unsigned char* smem, const E* __restrict__ keys,
+    const E* __restrict__ values, E* __restrict__ cache, const int32_t* __restrict__ kv_lens,
+    const int32_t* __restrict__ page_indices, const int32_t* __restrict__ cu,
+    const int32_t* __restrict__ dist, OutS* __restrict__ out, const int32_t* __restrict__ plan,
+    const float* __restrict__ part_o, const float* __restrict__ part_ml, bool merges,
+    int32_t nfin, int32_t fb, int pw) {
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const bool decode_on = p.decode_waves > 0;
+  const PlanView pv = plan_view(plan, p.S);
+  PlanCore& pl_core = *reinterpret_cast<PlanCore*>(smem);
+  PlanRows* pl_rows = reinterpret_cast<PlanRows*>(smem + sizeof(PlanCore));
+  int32_t n;
+  if (decode_on) {
+    n = min(max(pv.hdr[0], 0), p.S);
+  } else {
+    n = build_plan(p, kv_lens, cu, dist, 16, false, pl_core, pl_rows).num_seqs;
+  }
+  const int32_t total = merges ? (decode_on ? n * p.Hkv : 0) : (p.skip_kv_update ? 0 : p.T);
+  const int32_t nw = nfin * pw;
+  for (int32_t it = fb * pw + wave; it < total; it += nw) {
+    if (merges)
+      finish_merge_item<DP, OutS>(p, pv, it, part_o, part_ml, out);
+    else
+      finish_write_item<E>(p, decode_on, pv, pl_rows, n, cu, kv_lens, cache, page_indices, keys,
+                           values, it, lane);
+  }
+}
+
 // Two workgroups per CU at head_dim 128 (256 registers per lane), one at 256.
 // FULL_D: head_dim == Dp (no zero-padded dims to skip).
 template <typename KV, int DP, typename OutS, bool FULL_D>
@@ -130,10 +174,12 @@ __global__ void __launch_bounds__(PrefillCfg<DP>::THREADS) __attribute__((amdgpu
 prefill_kernel(Params p, const uint16_t* __restrict__ q,
                const typename KV::storage* __restrict__ keys,
                const typename KV::storage* __restrict__ values,
-               const typename KV::storage* __restrict__ cache,
+               typename KV::storage* __restrict__ cache,
                const int32_t* __restrict__ kv_lens, const int32_t* __restrict__ page_indices,
                const int32_t* __restrict__ cu, const int32_t* __restrict__ dist,
-               OutS* __restrict__ out, const int32_t* __restrict__ plan) {
+               OutS* __restrict__ out, const int32_t* __restrict__ plan,
+               const float* __restrict__ part_o, const float* __restrict__ part_ml,
+               int32_t nfm, int32_t nfw) {
   using C = PrefillCfg<DP>;
   using E = typename KV::storage;
   constexpr int BK = C::BK;
@@ -150,6 +196,20 @@ prefill_kernel(Params p, const uint16_t* __restrict__ q,
   const int half = lane >> 5;
   const bool decode_on = p.decode_waves > 0;
   const int32_t bq = C::ROWS / p.qpk;  // query tokens per item
+  // ---- finish workgroups: [0, nfm) merge items, the last nfw write items.
+  const int32_t blk_id = static_cast<int32_t>(blockIdx.x);
+  const int32_t nattn = static_cast<int32_t>(gridDim.x) - nfm - nfw;
+  if (blk_id < nfm || blk_id >= nfm + nattn) {
+    const bool merges = blk_id < nfm;
+    prefill_finish_role<E, DP, OutS>(p, smem, keys, values, cache, kv_lens, page_indices, cu,
+                                     dist, out, plan, part_o, part_ml, merges,
+                                     merges ? nfm : nfw, merges ? blk_id : blk_id - nfm - nattn,
+                                     C::THREADS / 64);
+    return;
+  }
+  // Attention block index (nfm is a multiple of 8, so bid % 8 and blockIdx.x
+  // % 8 -- the XCD the dispatcher picks -- agree).
+  const int32_t bid = blk_id - nfm;
   // The decode kernel counted the sequences with non-decode rows.
   if (decode_on && plan[3] == 0) return;
 
@@ -162,10 +222,10 @@ prefill_kernel(Params p, const uint16_t* __restrict__ q,
   __syncthreads();
   block_exclusive_scan(blk, n, red);
   const int32_t total = blk[n];
-  const int32_t h = static_cast<int32_t>(blockIdx.x % p.Hkv);
+  const int32_t h = bid % p.Hkv;
   // Later blocks of a sequence attend to more keys: walk blocks from the
   // last one so the longest items start first.
-  const int32_t kb_rev = static_cast<int32_t>(blockIdx.x / p.Hkv);
+  const int32_t kb_rev = bid / p.Hkv;
   if (kb_rev >= total) return;
   const int32_t kb = total - 1 - kb_rev;
   const int32_t s = find_prefix(blk, n, kb);
@@ -490,23 +550,27 @@ prefill_kernel(Params p, const uint16_t* __restrict__ q,
 }
 
 template <typename KV, typename OutS>
-hipError_t launch_dp(const Params& p, const void* q, const void* k, const void* v,
-                     const void* cache, const int32_t* kv_lens, const int32_t* page_indices,
-                     const int32_t* cu, const int32_t* dist, void* out, const int32_t* plan,
+hipError_t launch_dp(const Params& p, const void* q, const void* k, const void* v, void* cache,
+                     const int32_t* kv_lens, const int32_t* page_indices, const int32_t* cu,
+                     const int32_t* dist, void* out, const DecodeWorkspace& ws, int num_cus,
                      hipStream_t stream) {
   using E = typename KV::storage;
-  // Upper bound on items: every sequence adds at most one partial block.
+  // Upper bound on attention items: every sequence adds at most one partial
+  // block.
   const int32_t bq = (p.Dp == 128 ? PrefillCfg<128>::ROWS : PrefillCfg<256>::ROWS) / p.qpk;
   const int64_t blocks = (static_cast<int64_t>(p.T) + bq - 1) / bq + p.S;
-  const int64_t grid = blocks * p.Hkv;
+  const int32_t nfm = prefill_merge_blocks(p, num_cus);
+  const int32_t nfw = prefill_write_blocks(p, num_cus);
+  const int64_t grid = blocks * p.Hkv + nfm + nfw;
   if (grid > 0x7fffffff) return hipErrorInvalidValue;
   const dim3 g(static_cast<uint32_t>(grid));
 #define RPA_PREFILL_LAUNCH(DPV, FULL)                                                        \
   hipLaunchKernelGGL((prefill_kernel<KV, DPV, OutS, FULL>), g,                             \
                      dim3(PrefillCfg<DPV>::THREADS), 0, stream, p,                           \
                      static_cast<const uint16_t*>(q), static_cast<const E*>(k),             \
-                     static_cast<const E*>(v), static_cast<const E*>(cache), kv_lens,       \
-                     page_indices, cu, dist, static_cast<OutS*>(out), plan)
+                     static_cast<const E*>(v), static_cast<E*>(cache), kv_lens,             \
+                     page_indices, cu, dist, static_cast<OutS*>(out), ws.plan, ws.part_o,    \
+                     ws.part_ml, nfm, nfw)
   const bool full = p.D == p.Dp;
   if (p.Dp == 128) {
     if (full) RPA_PREFILL_LAUNCH(128, true); else RPA_PREFILL_LAUNCH(128, false);
@@ -521,16 +585,16 @@ hipError_t launch_dp(const Params& p, const void* q, const void* k, const void* 
 
 template <typename OutS>
 hipError_t launch_kv(const Params& p, int kv_dtype, const void* q, const void* k, const void* v,
-                     const void* cache, const int32_t* kv_lens, const int32_t* page_indices,
-                     const int32_t* cu, const int32_t* dist, void* out, const int32_t* plan,
-                     hipStream_t stream) {
+                     void* cache, const int32_t* kv_lens, const int32_t* page_indices,
+                     const int32_t* cu, const int32_t* dist, void* out, const DecodeWorkspace& ws,
+                     int num_cus, hipStream_t stream) {
   switch (kv_dtype) {
     case RPA_DTYPE_BF16:
-      return launch_dp<PKvBF16, OutS>(p, q, k, v, cache, kv_lens, page_indices, cu, dist, out, plan, stream);
+      return launch_dp<PKvBF16, OutS>(p, q, k, v, cache, kv_lens, page_indices, cu, dist, out, ws, num_cus, stream);
     case RPA_DTYPE_FP8_E4M3FN:
-      return launch_dp<PKvFP8<false>, OutS>(p, q, k, v, cache, kv_lens, page_indices, cu, dist, out, plan, stream);
+      return launch_dp<PKvFP8<false>, OutS>(p, q, k, v, cache, kv_lens, page_indices, cu, dist, out, ws, num_cus, stream);
     case RPA_DTYPE_FP8_E5M2:
-      return launch_dp<PKvFP8<true>, OutS>(p, q, k, v, cache, kv_lens, page_indices, cu, dist, out, plan, stream);
+      return launch_dp<PKvFP8<true>, OutS>(p, q, k, v, cache, kv_lens, page_indices, cu, dist, out, ws, num_cus, stream);
     default:
       return hipErrorInvalidValue;
   }
@@ -551,15 +615,32 @@ bool prefill_supported(const Params& p, int q_dtype, int kv_dtype, int out_dtype
   return true;
 }
 
+// Merge workgroups (front of the grid): one merge item per wavefront for
+// every possible pair, at most two per CU (the kernel's occupancy), a
+// multiple of 8 so the attention blocks keep their XCD placement.
+int prefill_merge_blocks(const Params& p, int num_cus) {
+  if (p.decode_waves <= 0) return 0;
+  int64_t b = (static_cast<int64_t>(p.S) * p.Hkv + 3) / 4;
+  b = b > 2 * num_cus ? 2 * num_cus : b;
+  return static_cast<int>((b + 7) / 8 * 8);
+}
+
+// Write workgroups (end of the grid): about 16 token rows each, at most one
+// per CU.
+int prefill_write_blocks(const Params& p, int num_cus) {
+  if (p.skip_kv_update || p.T == 0) return 0;
+  int64_t b = (static_cast<int64_t>(p.T) + 15) / 16;
+  return static_cast<int>(b > num_cus ? num_cus : b);
+}
+
 hipError_t launch_prefill(const Params& p, int kv_dtype, int out_dtype, const void* q,
-                          const void* k, const void* v, const void* cache,
-                          const int32_t* kv_lens, const int32_t* page_indices,
-                          const int32_t* cu, const int32_t* dist, void* out,
-                          const int32_t* plan, hipStream_t stream) {
-  if (p.decode_waves > 0 && plan == nullptr) return hipErrorInvalidValue;
+                          const void* k, const void* v, void* cache, const int32_t* kv_lens,
+                          const int32_t* page_indices, const int32_t* cu, const int32_t* dist,
+                          void* out, const DecodeWorkspace& ws, int num_cus, hipStream_t stream) {
+  if (p.decode_waves > 0 && ws.plan == nullptr) return hipErrorInvalidValue;
   if (out_dtype == RPA_DTYPE_F32)
-    return launch_kv<float>(p, kv_dtype, q, k, v, cache, kv_lens, page_indices, cu, dist, out, plan, stream);
-  return launch_kv<uint16_t>(p, kv_dtype, q, k, v, cache, kv_lens, page_indices, cu, dist, out, plan, stream);
+    return launch_kv<float>(p, kv_dtype, q, k, v, cache, kv_lens, page_indices, cu, dist, out, ws, num_cus, stream);
+  return launch_kv<uint16_t>(p, kv_dtype, q, k, v, cache, kv_lens, page_indices, cu, dist, out, ws, num_cus, stream);
 }
 
 }  // namespace rpa
