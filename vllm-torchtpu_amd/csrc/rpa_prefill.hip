@@ -1,10 +1,12 @@
 // Prefill attention (rows of sequences with several query tokens) for gfx950.
 //
-// MFMA flash attention over the paged cache.  A workgroup (4 wavefronts)
-// owns one item: 128 q rows of one sequence and one kv head -- BQ = 128 / qpk
-// consecutive query tokens times the qpk q heads that share the kv head (GQA
-// packing: the K/V tiles of the kv head are read once for all of them).
-// Wavefront w owns rows [32w, 32w + 32).  Keys are streamed in 32-key tiles,
+// MFMA flash attention over the paged cache.  A workgroup (8 wavefronts at
+// head_dim 128, 4 at 256) owns one item: 32 q rows per wavefront of one
+// sequence and one kv head -- BQ = rows / qpk consecutive query tokens times
+// the qpk q heads that share the kv head (GQA packing: the K/V tiles of the
+// kv head are read once for all of them).
+// Wavefront w owns rows [32w, 32w + 32).  Keys are streamed in 64-key tiles
+// (32 at head_dim 256),
 // staged through double-buffered LDS as bf16 (fp8 KV converted on the way),
 // the next tile's global loads in flight in registers while the current one
 // is consumed.
@@ -88,8 +90,10 @@ __device__ __forceinline__ float sum_bf16x2(uint32_t pair, float acc) {
 
 template <int DP>
 struct PrefillCfg {
-  // 4 wavefronts: two workgroups per CU at head_dim 128, one at 256.
-  static constexpr int THREADS = 256;
+  // head_dim 128: 8 wavefronts (256 q rows), one workgroup per CU with two
+  // wavefronts per SIMD -- each K|V tile staged once feeds twice the rows of
+  // a 4-wavefront workgroup.  head_dim 256: 4 wavefronts, one per SIMD.
+  static constexpr int THREADS = DP == 128 ? 512 : 256;
   static constexpr int ROWS = 32 * THREADS / 64;   // q rows per item (32 per wavefront)
   static constexpr int BK = DP == 128 ? 64 : 32;   // keys per tile
   static constexpr int NSB = BK / 32;              // 32-key S^T blocks per tile
@@ -167,7 +171,7 @@ __device__ __forceinline__ void prefill_finish_role(
   }
 }
 
-// Two workgroups per CU at head_dim 128 (256 registers per lane), one at 256.
+// Two wavefronts per SIMD at head_dim 128 (256 registers per lane), one at 256.
 // FULL_D: head_dim == Dp (no zero-padded dims to skip).
 template <typename KV, int DP, typename OutS, bool FULL_D>
 __global__ void __launch_bounds__(PrefillCfg<DP>::THREADS) __attribute__((amdgpu_waves_per_eu(DP == 128 ? 2 : 1)))
@@ -610,7 +614,8 @@ bool prefill_supported(const Params& p, int q_dtype, int kv_dtype, int out_dtype
   if (out_dtype != RPA_DTYPE_BF16 && out_dtype != RPA_DTYPE_F32) return false;
   if (p.Dp != 128 && p.Dp != 256) return false;
   // 8-element pieces of q / k / v rows; at least one query token per item.
-  if (p.D % 8 != 0 || p.qpk > PrefillCfg<256>::ROWS) return false;
+  if (p.D % 8 != 0 || p.qpk > (p.Dp == 128 ? PrefillCfg<128>::ROWS : PrefillCfg<256>::ROWS))
+    return false;
   if (p.S > kMaxDecodeSeqs) return false;
   return true;
 }
