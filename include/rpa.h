@@ -149,6 +149,33 @@ int rpa_forward(const rpa_desc* d, const void* queries, const void* keys,
                 const int32_t* distribution, void* out, void* workspace,
                 size_t workspace_bytes, void* stream);
 
+/* rpa_forward that also writes lse (f32 [max_num_tokens, num_q_heads],
+ * device memory): the natural-log log-sum-exp m + log(l) of every computed
+ * output row over the keys it attends (logits after sm_scale, k_scale,
+ * q_scale and the soft cap; -inf for a row that attends no key).  Rows of lse
+ * >= cu_q_lens[num_seqs] are left untouched.  Replaces the return_lse output
+ * of the batched RPA wrapper,
+ *   src/vllm_torchtpu/kernels/experimental/batched_rpa/wrapper.py:553, :610-623
+ *   (LSE = m + log(max(l, 1e-9)), batched_rpa/kernel.py:116-124),
+ * the partial results that context-parallel attention merges. */
+int rpa_forward_lse(const rpa_desc* d, const void* queries, const void* keys,
+                    const void* values, void* kv_cache, const int32_t* kv_lens,
+                    const int32_t* page_indices, const int32_t* cu_q_lens,
+                    const int32_t* distribution, void* out, float* lse, void* workspace,
+                    size_t workspace_bytes, void* stream);
+
+/* LSE-weighted merge of num_parts partial attentions of the same rows:
+ * outs [num_parts, rows, head_dim] and lses [num_parts, rows] (f32, natural
+ * log) -> out [rows, head_dim] and, when lse_out is not NULL, lse_out [rows].
+ * dtype (RPA_DTYPE_BF16 or RPA_DTYPE_F32) is that of outs and out; head_dim
+ * <= 512.  Replaces merge_attn_results,
+ *   src/vllm_torchtpu/layers/adapter/cp_attention.py:45-72
+ * (exactly, for num_parts = 2; NaN and +-inf partial outputs count as 0) and
+ * the local combine of cp_lse_ag_out_rs, distributed/dcp_comm.py:23-68. */
+int rpa_merge_attn_states(int32_t num_parts, int64_t rows, int32_t head_dim, int32_t dtype,
+                          const void* outs, const float* lses, void* out, float* lse_out,
+                          void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -28,6 +28,14 @@ Functions and what pins each one (the tests live in
   skip_kv_update invariant (`tests/kernels/test_rpa_skip_kv_update.py:169-182`).
 * `static_validate_inputs`, `dynamic_validate_inputs` -- kernel.py:1273-1538.
   Pinned by one table-driven test per `ValueError` condition.
+* `merge_attn_results`                           -- layers/adapter/cp_attention.py:45-72;
+  `merge_attn_states`, its R-partial generalisation.  Pinned by the split
+  identity (attention over a key set equals the merge of the attentions over
+  any partition of it, computed independently in fp64), closed forms (a
+  partial with lse -inf drops out; equal lses average) and R = 2 agreement.
+* `ref_ragged_paged_attention(..., return_lse=True)` -- the LSE is pinned
+  against a per-element fp64 log-sum-exp loop and closed forms (one key:
+  lse = its logit; constant logits c over n keys: c + log n).
 * `ref_ragged_paged_attention(mode=...)`         -- kernel.py:74-214.
   - mode="fp32"/"fp64": the same algorithm with every intermediate kept in
     fp32/fp64 (the BASELINE tolerance target).  Pinned by a per-element
@@ -323,10 +331,15 @@ def ref_ragged_paged_attention(
     out_dtype: Any = None, mask_value: float | None = None,
     q_scale: float | None = None, k_scale: float | None = None,
     v_scale: float | None = None, mode: str = "faithful", validate: bool = True,
+    return_lse: bool = False,
 ):
     """CPU restatement of ref_ragged_paged_attention (kernel.py:74-214).
 
-    Returns (out [cu_q_lens[num_seqs], Hq, D], new_kv_cache).  `mode`:
+    Returns (out [cu_q_lens[num_seqs], Hq, D], new_kv_cache), plus, with
+    return_lse (fp32/fp64 modes), lse [cu_q_lens[num_seqs], Hq]: the
+    natural-log log-sum-exp of each row's unmasked logits, the quantity the
+    batched RPA wrapper returns (batched_rpa/wrapper.py:610-623,
+    batched_rpa/kernel.py:116-124: m + log(l)).  `mode`:
       "faithful" -- the reference's cast points (kernel.py:185-209) in
                     torch's bf16/fp8 arithmetic.
       "fp32" / "fp64" -- identical algorithm, every intermediate in that
@@ -361,7 +374,9 @@ def ref_ragged_paged_attention(
     merged = torch.from_numpy(_int_view(merge_kv(keys, values)))
 
     acc_dtype = {"fp32": torch.float32, "fp64": torch.float64}.get(mode)
+    assert not (return_lse and mode == "faithful"), "return_lse needs mode fp32 or fp64"
     outputs = []
+    lses = []
     for i in range(num_seqs):
         q_start, q_end = int(cu_q_lens[i]), int(cu_q_lens[i + 1])
         q_len = q_end - q_start
@@ -425,6 +440,10 @@ def ref_ragged_paged_attention(
                 attn = attn * q_scale
             if soft_cap is not None:
                 attn = soft_cap * torch.tanh(attn / soft_cap)
+            if return_lse:
+                live = attn if mask is None else torch.where(
+                    mask, attn, torch.tensor(float("-inf"), dtype=acc_dtype))
+                lses.append(torch.logsumexp(live, dim=-1).transpose(0, 1))  # [q, h]
             if mask is not None:
                 attn = torch.where(mask, attn,
                                    torch.tensor(mask_value, dtype=acc_dtype))
@@ -439,7 +458,44 @@ def ref_ragged_paged_attention(
     else:
         rdt = out_dtype if mode == "faithful" else acc_dtype
         result = torch.empty((0, hq, d), dtype=rdt)
+    if return_lse:
+        lse = torch.cat(lses, dim=0) if lses else torch.empty((0, hq), dtype=acc_dtype)
+        return result, work.view(kv_dtype), lse
     return result, work.view(kv_dtype)
+
+
+def merge_attn_results(out_a, lse_a, out_b, lse_b):
+    """Restates merge_attn_results (layers/adapter/cp_attention.py:45-72): the
+    numerically stable LSE-weighted combination of two partial attentions,
+    out [T, H, D] and lse [T, H] (natural log) each."""
+    m = torch.maximum(lse_a, lse_b)
+    m_finite = torch.isfinite(m)
+    m_safe = torch.where(m_finite, m, torch.zeros_like(m))
+    ea = torch.exp(lse_a - m_safe)
+    eb = torch.exp(lse_b - m_safe)
+    norm = ea + eb
+    out_a = torch.nan_to_num(out_a, nan=0.0, posinf=0.0, neginf=0.0)
+    out_b = torch.nan_to_num(out_b, nan=0.0, posinf=0.0, neginf=0.0)
+    norm_safe = torch.where(norm > 0, norm, torch.ones_like(norm))
+    out = (ea.unsqueeze(-1) * out_a + eb.unsqueeze(-1) * out_b) / norm_safe.unsqueeze(-1)
+    lse_out = torch.where(m_finite, m + torch.log(norm_safe), m)
+    return out, lse_out
+
+
+def merge_attn_states(outs, lses):
+    """merge_attn_results generalised to R partials: outs [R, ..., D], lses
+    [R, ...]; the same max, finiteness, nan_to_num and zero-norm rules.  For
+    R = 2 it equals merge_attn_results."""
+    m = lses.max(dim=0).values
+    m_finite = torch.isfinite(m)
+    m_safe = torch.where(m_finite, m, torch.zeros_like(m))
+    e = torch.exp(lses - m_safe.unsqueeze(0))
+    norm = e.sum(dim=0)
+    outs = torch.nan_to_num(outs, nan=0.0, posinf=0.0, neginf=0.0)
+    norm_safe = torch.where(norm > 0, norm, torch.ones_like(norm))
+    out = (e.unsqueeze(-1) * outs).sum(dim=0) / norm_safe.unsqueeze(-1)
+    lse_out = torch.where(m_finite, m + torch.log(norm_safe), m)
+    return out, lse_out
 
 
 def _self_check():  # pragma: no cover - manual use

@@ -11,10 +11,12 @@ import torch
 
 def brute_force_rpa(q, k, v, kv_cache, kv_lens, page_indices, cu_q_lens, distribution, *,
                     sm_scale=1.0, sliding_window=None, soft_cap=None, k_scale=None,
-                    v_scale=None, use_causal_mask=True, skip_kv_update=False):
+                    v_scale=None, use_causal_mask=True, skip_kv_update=False,
+                    return_lse=False):
     """Per-element fp64 attention written directly from the semantic contract
     (positions, page table, K/V combined-head interleave), independent of the
-    oracle's gather/einsum code.  Returns [num_tokens, Hq, D] float64."""
+    oracle's gather/einsum code.  Returns [num_tokens, Hq, D] float64 (and,
+    with return_lse, the per-row log(sum_j exp(logit_j)) [num_tokens, Hq])."""
     Q = q.to(torch.float64).numpy()
     K = k.to(torch.float64).numpy()
     V = v.to(torch.float64).numpy()
@@ -30,6 +32,7 @@ def brute_force_rpa(q, k, v, kv_cache, kv_lens, page_indices, cu_q_lens, distrib
     kvl = [int(x) for x in kv_lens.tolist()]
     pt = [int(x) for x in page_indices.tolist()]
     out = np.zeros((cu[n], Hq, D))
+    lse = np.full((cu[n], Hq), -np.inf)
     for s in range(n):
         q0, ql, kl = cu[s], cu[s + 1] - cu[s], kvl[s]
         for i in range(ql):
@@ -64,6 +67,9 @@ def brute_force_rpa(q, k, v, kv_cache, kv_lens, page_indices, cu_q_lens, distrib
                 if v_scale is not None:
                     o = o * v_scale
                 out[q0 + i, gq] = o
+                lse[q0 + i, gq] = m + math.log(tot)
+    if return_lse:
+        return torch.from_numpy(out), torch.from_numpy(lse)
     return torch.from_numpy(out)
 
 

@@ -416,3 +416,89 @@ def test_algorithmic_bytes_formula():
     assert WL.prefill_flops(kvl, cu, 2, 8, 128) == 4 * 128 * 8 * (5 + 6 + 7)
     assert math.isclose(WL.algorithmic_flops([10], [0, 4], 1, 1, 1, sliding_window=8),
                         4 * (7 + 8 + 8 + 8))
+
+
+# ---------------------------------------------------------------------------
+# LSE output and the LSE merge (batched_rpa/wrapper.py:610-623,
+# layers/adapter/cp_attention.py:45-72)
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("case", range(len(BRUTE_CASES)))
+def test_oracle_lse_vs_bruteforce(case):
+    c = dict(BRUTE_CASES[case])
+    seq_lens, hq, hkv, d, ps = (c.pop(x) for x in ("seq_lens", "hq", "hkv", "d", "ps"))
+    w = wl(seq_lens, hq, hkv, d, ps, kv_dtype=E4M3, seed=31 + case, k_scale=0.75,
+           v_scale=1.5, **c)
+    out, _, lse = O.ref_ragged_paged_attention(*w.args(), mode="fp64", return_lse=True,
+                                               **w.kwargs)
+    bf_out, bf_lse = brute_force_rpa(*w.args(), return_lse=True, **w.kwargs)
+    assert_close(out, bf_out, 1e-10, 1e-10, "out")
+    assert_close(lse, bf_lse, 1e-10, 1e-10, "lse")
+
+
+def test_lse_closed_forms():
+    # One key: lse is that key's logit.
+    w = wl([(1, 1)], 2, 1, 16, 16, seed=41)
+    _, _, lse = O.ref_ragged_paged_attention(*w.args(), mode="fp64", return_lse=True,
+                                             **w.kwargs)
+    logit = (w.q[0].double() @ w.k[0, 0].double()) * w.kwargs["sm_scale"]
+    assert_close(lse[0], logit, 1e-12, 0, "single key")
+    # q = 0: every logit is 0, so lse = log(number of attended keys).
+    w = wl([(3, 20), (1, 9)], 4, 2, 32, 8, seed=42, sliding_window=5)
+    w.q.zero_()
+    _, _, lse = O.ref_ragged_paged_attention(*w.args(), mode="fp64", return_lse=True,
+                                             **w.kwargs)
+    counts = torch.tensor([5.0, 5.0, 5.0, 5.0], dtype=torch.float64)  # window 5 everywhere
+    assert_close(lse, counts.log().view(-1, 1).expand(4, 4), 1e-12, 0, "log n")
+
+
+def _partial(q, k, v, idx, scale):
+    """fp64 attention of q [H, D] over keys idx of k/v [n, D]: (out, lse)."""
+    s = (q @ k[idx].T) * scale                      # [H, m]
+    lse = torch.logsumexp(s, dim=-1)
+    out = torch.softmax(s, dim=-1) @ v[idx]
+    return out, lse
+
+
+def test_merge_split_identity():
+    """Attention over a key set equals the merge of the attentions over any
+    partition of it: the identity context-parallel decoding relies on."""
+    g = torch.Generator().manual_seed(43)
+    H, D, n = 6, 32, 50
+    q = torch.randn(H, D, generator=g, dtype=torch.float64)
+    k = torch.randn(n, D, generator=g, dtype=torch.float64)
+    v = torch.randn(n, D, generator=g, dtype=torch.float64)
+    full_out, full_lse = _partial(q, k, v, torch.arange(n), 0.3)
+    perm = torch.randperm(n, generator=g)
+    a, b, c = perm[:7], perm[7:31], perm[31:]
+    pa, pb, pc = (_partial(q, k, v, i, 0.3) for i in (a, b, c))
+    out2, lse2 = O.merge_attn_results(*_partial(q, k, v, perm[:20], 0.3),
+                                      *_partial(q, k, v, perm[20:], 0.3))
+    assert_close(out2, full_out, 1e-12, 1e-12, "two-way")
+    assert_close(lse2, full_lse, 1e-12, 1e-12, "two-way lse")
+    out3, lse3 = O.merge_attn_states(torch.stack([pa[0], pb[0], pc[0]]),
+                                     torch.stack([pa[1], pb[1], pc[1]]))
+    assert_close(out3, full_out, 1e-12, 1e-12, "three-way")
+    assert_close(lse3, full_lse, 1e-12, 1e-12, "three-way lse")
+    # R = 2 of the generalisation is the reference function.
+    o_s, l_s = O.merge_attn_states(torch.stack([pa[0], pb[0]]), torch.stack([pa[1], pb[1]]))
+    o_r, l_r = O.merge_attn_results(pa[0], pa[1], pb[0], pb[1])
+    assert torch.equal(o_s, o_r) and torch.equal(l_s, l_r)
+
+
+def test_merge_closed_forms():
+    g = torch.Generator().manual_seed(44)
+    out_a = torch.randn(3, 2, 8, generator=g, dtype=torch.float64)
+    lse_a = torch.randn(3, 2, generator=g, dtype=torch.float64)
+    # A partial with lse -inf (no keys) drops out, even with a NaN output.
+    out_b = torch.full_like(out_a, float("nan"))
+    lse_b = torch.full_like(lse_a, float("-inf"))
+    o, l = O.merge_attn_results(out_a, lse_a, out_b, lse_b)
+    assert_close(o, out_a, 0, 0)
+    assert_close(l, lse_a, 0, 0)
+    # Equal lses average the outputs and add log 2.
+    o, l = O.merge_attn_results(out_a, lse_a, -out_a, lse_a)
+    assert_close(o, torch.zeros_like(o), 1e-15, 0)
+    assert_close(l, lse_a + math.log(2.0), 1e-15, 1e-15)
+    # Both partials empty: output 0, lse -inf.
+    o, l = O.merge_attn_results(out_b, lse_b, out_b, lse_b)
+    assert torch.equal(o, torch.zeros_like(o)) and bool(torch.isneginf(l).all())

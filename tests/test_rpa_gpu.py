@@ -340,3 +340,98 @@ def test_non_positive_sm_scale(gpu_device, scale):
     check(W.make_workload([(1, 70), (9, 40), (33, 33)], 8, 2, 128, 16, seed=40,
                           distribution=[1, 1, 3], name=f"scale{scale}", sm_scale=scale),
           gpu_device)
+
+
+# ---------------------------------------------------------------------------
+# return_lse and the LSE merge (batched_rpa/wrapper.py:553, :610-623;
+# layers/adapter/cp_attention.py:45-72)
+# ---------------------------------------------------------------------------
+LSE_CASES = [
+    ("decode", dict(seq_lens=DECODE16, hq=32, hkv=8, d=128, ps=16,
+                    distribution=[16, 16, 16])),
+    ("mixed", dict(seq_lens=MIXED16, hq=32, hkv=8, d=128, ps=16)),
+    ("window-cap", dict(seq_lens=[(1, 700), (40, 300), (1, 5)], hq=16, hkv=4, d=128, ps=16,
+                        sliding_window=128, soft_cap=30.0)),
+    ("d256", dict(seq_lens=[(1, 500), (33, 90)], hq=16, hkv=8, d=256, ps=16)),
+    ("fp8", dict(seq_lens=[(1, 900), (17, 80)], hq=32, hkv=8, d=128, ps=32,
+                 kv_dtype=E4M3, k_scale=0.7, v_scale=1.3)),
+    ("generic-qpk24", dict(seq_lens=[(1, 300), (9, 40)], hq=24, hkv=1, d=128, ps=16)),
+    ("f32", dict(seq_lens=[(1, 70), (5, 20)], hq=8, hkv=2, d=64, ps=16,
+                 q_dtype=torch.float32, kv_dtype=torch.float32)),
+]
+
+
+@pytest.mark.parametrize("name", [c[0] for c in LSE_CASES])
+def test_return_lse(gpu_device, name):
+    c = dict(dict(LSE_CASES)[name])
+    seq_lens, hq, hkv, d, ps = (c.pop(x) for x in ("seq_lens", "hq", "hkv", "d", "ps"))
+    w = W.make_workload(seq_lens, hq, hkv, d, ps, seed=51, name=f"lse-{name}", **c)
+    _log(f"[rpa-gpu] return_lse {name}")
+    exp_out, exp_cache, exp_lse = O.ref_ragged_paged_attention(*w.args(), mode="fp32",
+                                                               return_lse=True, **w.kwargs)
+    g = w.to(gpu_device)
+    out, cache, lse = R.ragged_paged_attention(*g.args(), return_lse=True, **w.kwargs)
+    torch.cuda.synchronize()
+    n = w.num_tokens
+    tol = TOL[w.kv_cache.dtype]
+    assert_close(out[:n].cpu(), exp_out, tol, tol, f"{name} output")
+    # The LSE is an fp32 reduction of fp32 logits on both sides.
+    assert_close(lse[:n].cpu(), exp_lse, 1e-3, 1e-3, f"{name} lse")
+    assert bool(torch.isneginf(lse[n:]).all()), "rows past the batch keep lse -inf"
+    assert bytes_equal(cache.cpu(), exp_cache)
+
+
+@pytest.mark.parametrize("parts,dt", [(2, BF16), (3, torch.float32), (5, BF16), (70, torch.float32)])
+def test_merge_attn_states_gpu(gpu_device, parts, dt):
+    g = torch.Generator().manual_seed(52)
+    T, H, D = 37, 6, 128
+    outs = torch.randn(parts, T, H, D, generator=g).to(dt)
+    lses = torch.randn(parts, T, H, generator=g) * 3
+    lses[0, :5] = float("-inf")          # empty partials
+    outs[0, :5] = float("nan")           # ... whose outputs are garbage
+    lses[:, 7] = float("-inf")           # a row with no keys anywhere
+    exp_out, exp_lse = O.merge_attn_states(outs.double(), lses.double())
+    out, lse = R.merge_attn_states(outs.to(gpu_device), lses.to(gpu_device))
+    torch.cuda.synchronize()
+    tol = 2e-2 if dt == BF16 else 1e-5
+    assert_close(out.cpu(), exp_out, tol, tol, "merged output")
+    assert_close(lse.cpu(), exp_lse, 1e-5, 1e-5, "merged lse")
+    if parts == 2:
+        o2, l2 = R.merge_attn_results(outs[0].to(gpu_device), lses[0].to(gpu_device),
+                                      outs[1].to(gpu_device), lses[1].to(gpu_device))
+        assert torch.equal(o2.cpu(), out.cpu()) and torch.equal(l2.cpu(), lse.cpu())
+
+
+def test_dcp_split_merge_equals_full(gpu_device):
+    """Context-parallel decode on one GPU: each sequence's keys are split at a
+    page boundary into two shards (two calls over the same cache with their
+    own kv_lens and page-table offsets, skip_kv_update), and the LSE merge of
+    the shards equals attention over all keys (cp_attention.py:274-348)."""
+    ps = 16
+    kvl = [4000, 1000, 33, 2500]
+    w = W.make_workload([(1, k) for k in kvl], 32, 8, 128, ps, seed=53, name="dcp")
+    kw = dict(w.kwargs)
+    exp_out, _ = O.ref_ragged_paged_attention(*w.args(), mode="fp32", skip_kv_update=True, **kw)
+    g = w.to(gpu_device)
+    S = len(kvl)
+    pps = w.page_indices.shape[0] // S
+    split = [O.cdiv(k, 2 * ps) * ps for k in kvl]          # shard A: keys [0, split)
+    lens_a = torch.tensor(split, dtype=torch.int32)
+    lens_b = torch.tensor([k - s for k, s in zip(kvl, split)], dtype=torch.int32)
+    pt = w.page_indices.view(S, pps)
+    pt_b = torch.zeros_like(pt)
+    for s in range(S):
+        off = split[s] // ps
+        pt_b[s, :pps - off] = pt[s, off:]
+    outs, lses = [], []
+    for lens, table in ((lens_a, pt), (lens_b, pt_b)):
+        assert bool((lens > 0).all())
+        o, _, l = R.ragged_paged_attention(g.q, g.k, g.v, g.kv_cache, lens.to(gpu_device),
+                                           table.reshape(-1).contiguous().to(gpu_device),
+                                           g.cu_q_lens, g.distribution, skip_kv_update=True,
+                                           return_lse=True, **kw)
+        outs.append(o)
+        lses.append(l)
+    merged, _ = R.merge_attn_results(outs[0], lses[0], outs[1], lses[1])
+    torch.cuda.synchronize()
+    assert_close(merged[:S].cpu(), exp_out, 2e-2, 2e-2, "merged shards vs full attention")

@@ -9,6 +9,8 @@ from .rpa import (
     RpaCase,
     dynamic_validate_inputs,
     get_kv_cache_shape,
+    merge_attn_results,
+    merge_attn_states,
     merge_kv,
     ragged_paged_attention,
     ragged_paged_attention_bundled,
@@ -24,6 +26,8 @@ __all__ = [
     "dynamic_validate_inputs",
     "get_dtype_packing",
     "get_kv_cache_shape",
+    "merge_attn_results",
+    "merge_attn_states",
     "merge_kv",
     "next_power_of_2",
     "quantize_kv",

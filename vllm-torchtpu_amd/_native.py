@@ -53,6 +53,8 @@ EXPORTED_SYMBOLS = (
     "rpa_workspace_size",
     "rpa_kv_cache_update",
     "rpa_forward",
+    "rpa_forward_lse",
+    "rpa_merge_attn_states",
 )
 
 
@@ -122,6 +124,11 @@ def lib() -> ctypes.CDLL:
     L.rpa_kv_cache_update.argtypes = [desc_p] + [P] * 8
     L.rpa_forward.restype = ctypes.c_int
     L.rpa_forward.argtypes = [desc_p] + [P] * 10 + [ctypes.c_size_t, P]
+    L.rpa_forward_lse.restype = ctypes.c_int
+    L.rpa_forward_lse.argtypes = [desc_p] + [P] * 11 + [ctypes.c_size_t, P]
+    L.rpa_merge_attn_states.restype = ctypes.c_int
+    L.rpa_merge_attn_states.argtypes = [ctypes.c_int32, ctypes.c_int64, ctypes.c_int32,
+                                        ctypes.c_int32, P, P, P, P, P]
     if L.rpa_abi_version() != ABI_VERSION:
         raise NativeLibraryMissing(
             f"librpa_hip.so ABI {L.rpa_abi_version()} != expected {ABI_VERSION}; rebuild it")

@@ -168,6 +168,14 @@ int rpa_forward(const rpa_desc* d, const void* queries, const void* keys, const 
                 void* kv_cache, const int32_t* kv_lens, const int32_t* page_indices,
                 const int32_t* cu_q_lens, const int32_t* distribution, void* out,
                 void* workspace, size_t workspace_bytes, void* stream) {
+  return rpa_forward_lse(d, queries, keys, values, kv_cache, kv_lens, page_indices, cu_q_lens,
+                         distribution, out, nullptr, workspace, workspace_bytes, stream);
+}
+
+int rpa_forward_lse(const rpa_desc* d, const void* queries, const void* keys, const void* values,
+                    void* kv_cache, const int32_t* kv_lens, const int32_t* page_indices,
+                    const int32_t* cu_q_lens, const int32_t* distribution, void* out, float* lse,
+                    void* workspace, size_t workspace_bytes, void* stream) {
   const int st = rpa_validate_desc(d);
   if (st != RPA_OK) return st;
   if (d->max_num_tokens == 0) return RPA_OK;
@@ -182,6 +190,7 @@ int rpa_forward(const rpa_desc* d, const void* queries, const void* keys, const 
   if (align & 15u) return RPA_ERR_INVALID_ARG;
   hipStream_t s = static_cast<hipStream_t>(stream);
   rpa::Params p = make_params(d);
+  p.lse = lse;
   const bool decode_only = d->path == RPA_PATH_DECODE_ONLY;
   if (decode_only && !use_decode_kernel(d, p)) return RPA_ERR_UNSUPPORTED;
   if (!use_fused_path(d, p)) {

@@ -36,7 +36,18 @@ struct Params {
   int32_t skip_kv_update;  // new tokens are already in the cache (read them from there)
   int32_t decode_waves;    // wavefronts of the decode kernel's persistent grid (0: no decode kernel)
   int32_t prefill_on;      // the prefill kernel attends the non-decode rows
+  float* lse;              // [T, Hq] natural-log LSE of each output row, or null
 };
+
+constexpr float kLn2 = 0.6931471805599453f;
+
+// LSE of a row from its running max m (log2 units of the logits) and the sum
+// l of 2^(s - m): (m + log2 l) ln 2, natural-log base; -inf for a row that
+// attends no key (l == 0), as the reference's m + log(max(l, 1e-9)) with
+// m = -inf gives (batched_rpa/kernel.py:116-124).
+__device__ __forceinline__ float lse_from_log2(float m, float l) {
+  return l > 0.0f ? (m + __log2f(l)) * kLn2 : -INFINITY;
+}
 
 // Page and slot of logical position j (>= 0): shifts for power-of-two page
 // sizes (a wavefront-uniform branch), division otherwise.

@@ -480,7 +480,9 @@ decode_kernel(Params p, const uint16_t* __restrict__ q, const typename KV::stora
       if (last_tile && cur.lt0 == 0) {
         if (n < rows) {
           const float inv = (lsum == 0.0f) ? 0.0f : p.v_scale / lsum;
-          OutS* orow = out + ((static_cast<int64_t>(tq_cur) * p.Hq + h * p.qpk + n) * p.D);
+          const int64_t orow_i = static_cast<int64_t>(tq_cur) * p.Hq + h * p.qpk + n;
+          if (p.lse != nullptr && g == 0) p.lse[orow_i] = lse_from_log2(m_run, lsum);
+          OutS* orow = out + orow_i * p.D;
 #pragma unroll
           for (int t = 0; t < NT; ++t)
 #pragma unroll

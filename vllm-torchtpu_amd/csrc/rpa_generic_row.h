@@ -114,6 +114,8 @@ __device__ __forceinline__ void generic_row(const Params& p, const float* qs,
   }
 
   const float inv_l = (l_run == 0.0f) ? 0.0f : p.v_scale / l_run;
+  if (p.lse != nullptr && lane == 0)
+    p.lse[static_cast<int64_t>(t) * p.Hq + g] = l_run > 0.0f ? m_run + __logf(l_run) : -INFINITY;
   OutS* orow = out + (static_cast<int64_t>(t) * p.Hq + g) * p.D;
 #pragma unroll
   for (int c = 0; c < kGenericMaxChunks; ++c) {

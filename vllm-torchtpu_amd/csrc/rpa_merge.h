@@ -82,6 +82,11 @@ __device__ __forceinline__ void merge_partials(const Params& p, const float* __r
   float scale[RP];
 #pragma unroll
   for (int r = 0; r < RP; ++r) scale[r] = (L[r] == 0.0f) ? 0.0f : p.v_scale / L[r];
+  if (p.lse != nullptr) {
+#pragma unroll
+    for (int r = 0; r < RP; ++r)
+      if (lane == r && r < rows) p.lse[orow0 + r] = lse_from_log2(M[r], L[r]);
+  }
 
   float acc[NDW];
 #pragma unroll

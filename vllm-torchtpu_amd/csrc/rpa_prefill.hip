@@ -532,7 +532,10 @@ prefill_kernel(Params p, const uint16_t* __restrict__ q,
   const float lsum = l_run + __shfl_xor(l_run, 32, 64);
   if (!row_ok) return;
   const float inv = (lsum == 0.0f) ? 0.0f : p.v_scale / lsum;
-  OutS* orow = out + (static_cast<int64_t>(q_start + tok) * p.Hq + qhead) * p.D;
+  const int64_t orow_i = static_cast<int64_t>(q_start + tok) * p.Hq + qhead;
+  // Lanes l and l + 32 hold the same row.
+  if (p.lse != nullptr && half == 0) p.lse[orow_i] = lse_from_log2(m_ref, lsum);
+  OutS* orow = out + orow_i * p.D;
 #pragma unroll
   for (int tt = 0; tt < C::NT; ++tt)
 #pragma unroll

@@ -45,6 +45,8 @@ __all__ = [
     "ragged_paged_attention",
     "ragged_paged_attention_bundled",
     "rpa_kv_cache_update",
+    "merge_attn_results",
+    "merge_attn_states",
 ]
 
 
@@ -290,7 +292,7 @@ def _workspace(device: torch.device, nbytes: int) -> torch.Tensor:
 def _rpa_forward_impl(queries, keys, values, kv_cache, kv_lens, page_indices, cu_q_lens,
                       distribution, out, *, use_causal_mask, skip_kv_update, sm_scale,
                       sliding_window, soft_cap, q_scale, k_scale, v_scale,
-                      path=N.RPA_PATH_AUTO, workspace=None):
+                      path=N.RPA_PATH_AUTO, workspace=None, lse=None):
     L = N.lib()
     _require_device(queries, keys, values, kv_cache, kv_lens, page_indices, cu_q_lens,
                     distribution, out)
@@ -312,10 +314,20 @@ def _rpa_forward_impl(queries, keys, values, kv_cache, kv_lens, page_indices, cu
         elif workspace.numel() < ws_bytes:
             raise ValueError(f"workspace has {workspace.numel()} bytes, needs {ws_bytes}")
         stream = torch.cuda.current_stream(queries.device).cuda_stream
-        code = L.rpa_forward(desc, _ptr(queries), _ptr(keys), _ptr(values), _ptr(kv_cache),
-                             _ptr(kv_lens), _ptr(page_indices), _ptr(cu_q_lens),
-                             _ptr(distribution), _ptr(out), _ptr(workspace),
-                             ws_bytes, stream)
+        if lse is None:
+            code = L.rpa_forward(desc, _ptr(queries), _ptr(keys), _ptr(values), _ptr(kv_cache),
+                                 _ptr(kv_lens), _ptr(page_indices), _ptr(cu_q_lens),
+                                 _ptr(distribution), _ptr(out), _ptr(workspace),
+                                 ws_bytes, stream)
+        else:
+            if (lse.dtype != torch.float32 or not lse.is_contiguous() or lse.device != out.device
+                    or tuple(lse.shape) != tuple(queries.shape[:2])):
+                raise ValueError(f"lse must be a contiguous f32 {tuple(queries.shape[:2])} "
+                                 f"tensor on {out.device}")
+            code = L.rpa_forward_lse(desc, _ptr(queries), _ptr(keys), _ptr(values),
+                                     _ptr(kv_cache), _ptr(kv_lens), _ptr(page_indices),
+                                     _ptr(cu_q_lens), _ptr(distribution), _ptr(out), _ptr(lse),
+                                     _ptr(workspace), ws_bytes, stream)
     N.check(code, "rpa_forward")
     return out
 
@@ -343,6 +355,36 @@ def _(queries, keys, values, kv_cache, kv_lens, page_indices, cu_q_lens, distrib
       out_dtype, use_causal_mask, skip_kv_update, sm_scale, sliding_window, soft_cap,
       has_soft_cap, q_scale, k_scale, v_scale, path):
     return torch.empty(queries.shape, dtype=out_dtype, device=queries.device)
+
+
+# The same op with the LSE output (return_lse=True), as the batched RPA
+# wrapper's return_lse (batched_rpa/wrapper.py:553, :610-623).
+@torch.library.custom_op("rpa_amd::ragged_paged_attention_lse", mutates_args=("kv_cache",))
+def _rpa_lse_op(queries: torch.Tensor, keys: torch.Tensor, values: torch.Tensor,
+                kv_cache: torch.Tensor, kv_lens: torch.Tensor, page_indices: torch.Tensor,
+                cu_q_lens: torch.Tensor, distribution: torch.Tensor, out_dtype: torch.dtype,
+                use_causal_mask: bool, skip_kv_update: bool, sm_scale: float,
+                sliding_window: int, soft_cap: float, has_soft_cap: bool, q_scale: float,
+                k_scale: float, v_scale: float,
+                path: int) -> tuple[torch.Tensor, torch.Tensor]:
+    out = torch.empty(queries.shape, dtype=out_dtype, device=queries.device)
+    lse = torch.full(queries.shape[:2], float("-inf"), dtype=torch.float32,
+                     device=queries.device)
+    _rpa_forward_impl(
+        queries, keys, values, kv_cache, kv_lens, page_indices, cu_q_lens, distribution, out,
+        use_causal_mask=use_causal_mask, skip_kv_update=skip_kv_update, sm_scale=sm_scale,
+        sliding_window=sliding_window if sliding_window > 0 else None,
+        soft_cap=soft_cap if has_soft_cap else None, q_scale=q_scale, k_scale=k_scale,
+        v_scale=v_scale, path=path, lse=lse)
+    return out, lse
+
+
+@_rpa_lse_op.register_fake
+def _(queries, keys, values, kv_cache, kv_lens, page_indices, cu_q_lens, distribution,
+      out_dtype, use_causal_mask, skip_kv_update, sm_scale, sliding_window, soft_cap,
+      has_soft_cap, q_scale, k_scale, v_scale, path):
+    return (torch.empty(queries.shape, dtype=out_dtype, device=queries.device),
+            torch.empty(queries.shape[:2], dtype=torch.float32, device=queries.device))
 
 
 def ragged_paged_attention(
@@ -375,6 +417,7 @@ def ragged_paged_attention(
     debug_mode: bool = False,
     disable_bounds_checks: bool = True,
     disable_semaphore_checks: bool = True,
+    return_lse: bool = False,
 ):
     """Ragged paged attention with mixed prefill and decode (kernel.py:1633-1984).
 
@@ -382,6 +425,12 @@ def ragged_paged_attention(
     updated in place with the new tokens' K/V (unless skip_kv_update) and
     returned.  Rows of `out` at or beyond cu_q_lens[distribution[2]] are not
     written.  See the module docstring for the deliberate differences.
+
+    return_lse (an addition from the batched RPA wrapper, batched_rpa/
+    wrapper.py:553, :610-623): also return lse, f32 [max_num_tokens, Hq], the
+    natural-log log-sum-exp m + log(l) of each computed row's logits (after
+    scaling and soft cap; -inf for a row without keys, and for rows past
+    cu_q_lens[distribution[2]]) -- what merge_attn_results combines.
     """
     del debug_mode, disable_bounds_checks, disable_semaphore_checks
     static_validate_inputs(
@@ -404,14 +453,59 @@ def ragged_paged_attention(
         # cast to the KV dtype; q_scale is multiplied back into the logits.
         info = torch.finfo(kv_cache.dtype)
         q = torch.clamp(q / q_scale, min=info.min, max=info.max).to(kv_cache.dtype)
-    out = torch.ops.rpa_amd.ragged_paged_attention(
+    op = (torch.ops.rpa_amd.ragged_paged_attention_lse if return_lse
+          else torch.ops.rpa_amd.ragged_paged_attention)
+    res = op(
         q.contiguous(), keys.contiguous(), values.contiguous(), kv_cache, kv_lens, page_indices,
         cu_q_lens, distribution, result_dtype, bool(use_causal_mask), bool(skip_kv_update),
         float(sm_scale), 0 if sliding_window is None else int(sliding_window),
         0.0 if soft_cap is None else float(soft_cap), soft_cap is not None,
         1.0 if q_scale is None else float(q_scale), 1.0 if k_scale is None else float(k_scale),
         1.0 if v_scale is None else float(v_scale), N.RPA_PATH_AUTO)
-    return out, kv_cache
+    if return_lse:
+        out, lse = res
+        return out, kv_cache, lse
+    return res, kv_cache
+
+
+def merge_attn_states(outs: torch.Tensor, lses: torch.Tensor):
+    """LSE-weighted merge of R partial attentions of the same rows.
+
+    outs [R, ..., D] (bf16 or f32), lses [R, ...] (natural-log LSE, any float
+    dtype; computed in f32) -> (out [..., D] in outs.dtype, lse [...] f32).
+    merge_attn_results (cp_attention.py:45-72) generalised to R partials, on
+    the GPU (rpa_merge_attn_states in include/rpa.h): weights exp(lse_r - m)
+    with m = max_r lse_r, NaN/inf partial outputs counted as 0, rows whose
+    partials all have lse -inf give 0 and lse -inf.
+    """
+    if outs.dim() < 2 or lses.shape != outs.shape[:-1]:
+        raise ValueError(f"outs {tuple(outs.shape)} and lses {tuple(lses.shape)} do not match")
+    if not outs.is_cuda or lses.device != outs.device:
+        raise RuntimeError("merge_attn_states: tensors must be on one GPU (no CPU fallback)")
+    parts, dim = outs.shape[0], outs.shape[-1]
+    rows = outs[0].numel() // max(dim, 1)
+    outs_c = outs.contiguous()
+    lses_c = lses.to(torch.float32).contiguous()
+    out = torch.empty(outs.shape[1:], dtype=outs.dtype, device=outs.device)
+    lse = torch.empty(lses.shape[1:], dtype=torch.float32, device=outs.device)
+    L = N.lib()
+    with torch.cuda.device(outs.device):
+        stream = torch.cuda.current_stream(outs.device).cuda_stream
+        code = L.rpa_merge_attn_states(parts, rows, dim, N.rpa_dtype(outs.dtype), _ptr(outs_c),
+                                       _ptr(lses_c), _ptr(out), _ptr(lse), stream)
+    N.check(code, "rpa_merge_attn_states")
+    return out, lse
+
+
+def merge_attn_results(out_a: torch.Tensor, lse_a: torch.Tensor, out_b: torch.Tensor,
+                       lse_b: torch.Tensor):
+    """Numerically stable LSE-weighted combination of two partial attentions
+    (cp_attention.py:45-72): out [T, H, D], lse [T, H] (natural log) each;
+    returns (combined_out, combined_lse f32)."""
+    if out_a.shape != out_b.shape or lse_a.shape != lse_b.shape:
+        raise ValueError("merge_attn_results: partials differ in shape")
+    return merge_attn_states(torch.stack([out_a, out_b]),
+                             torch.stack([lse_a.to(torch.float32), lse_b.to(torch.float32)]))
 
 
 def ragged_paged_attention_bundled(queries, keys, values, kv_cache_bundle, layer_idx,
