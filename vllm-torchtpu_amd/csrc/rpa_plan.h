@@ -109,9 +109,10 @@ __device__ __forceinline__ int32_t decode_tiles(const Params& p, int32_t dkv, in
   return (hi - lo + tile - 1) / tile;
 }
 
-// Builds the plan in LDS (all threads of a kPlanThreads-wide workgroup take
-// part; ends with a barrier).  With decode_enabled false no sequence is a
-// decode sequence (every row belongs to the finish kernel).  R, when given,
+// Builds the plan in LDS (every thread of a workgroup of at least
+// kPlanThreads threads calls it; ends with a barrier).  With decode_enabled
+// false no sequence is a decode sequence (every row belongs to the finish
+// kernel).  R, when given,
 // receives every sequence's kv_len and cu_q_lens.
 template <typename PlanLds>
 __device__ __forceinline__ Plan build_plan(const Params& p, const int32_t* kv_lens,
@@ -122,7 +123,10 @@ __device__ __forceinline__ Plan build_plan(const Params& p, const int32_t* kv_le
   const int32_t n = min(num_seqs_of(dist, p.S), PlanLds::kCap);
   pl.num_seqs = n;
   int32_t tiles = 0, seqs = 0, others = 0;
-  for (int32_t s = tid; s < n; s += kPlanThreads) {
+  // Wider workgroups (the prefill kernel's 512 threads) take part with their
+  // first kPlanThreads threads only: the reduction slots hold kPlanWaves waves.
+  const bool planner = tid < kPlanThreads;
+  for (int32_t s = planner ? tid : n; s < n; s += kPlanThreads) {
     int32_t kl;
     const bool dec = is_decode_seq(p, cu, kv_lens, s, &kl) && decode_enabled;
     const int32_t nt = dec ? decode_tiles(p, kl, tile) : 0;
@@ -143,7 +147,7 @@ __device__ __forceinline__ Plan build_plan(const Params& p, const int32_t* kv_le
     seqs += __shfl_xor(seqs, o, 64);
     others += __shfl_xor(others, o, 64);
   }
-  if ((tid & 63) == 0) {
+  if (planner && (tid & 63) == 0) {
     L.red[tid >> 6] = tiles;
     L.red[kPlanWaves + (tid >> 6)] = seqs;
     L.red[2 * kPlanWaves + (tid >> 6)] = others;
