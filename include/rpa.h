@@ -88,11 +88,12 @@ typedef struct rpa_desc {
   int32_t num_q_heads;
   int32_t num_kv_heads;
   int32_t head_dim;        /* actual head_dim of q/k/v            */
-  int32_t head_dim_padded; /* align(head_dim, 128): cache last axis */
+  int32_t head_dim_padded; /* align(head_dim, 128): cache last axis (64: hd64 packed) */
   int32_t total_num_pages;
   int32_t page_size;
   int32_t kv_packing;      /* 32 / bits(kv_dtype)                  */
-  int32_t kv_heads_x2;     /* align(2 * num_kv_heads, kv_packing)  */
+  int32_t kv_heads_x2;     /* align(2 * num_kv_heads, kv_packing); hd64 packed:
+                              2 * align(num_kv_heads, kv_packing) */
   int32_t max_num_seqs;
   int32_t pages_per_seq;
   int32_t use_causal_mask; /* bool */
@@ -163,6 +164,23 @@ int rpa_forward_lse(const rpa_desc* d, const void* queries, const void* keys,
                     const int32_t* page_indices, const int32_t* cu_q_lens,
                     const int32_t* distribution, void* out, float* lse, void* workspace,
                     size_t workspace_bytes, void* stream);
+
+/* rpa_forward with the optional outputs and inputs of the reference's kernel
+ * variants.  attention_sink (f32 [num_q_heads], device memory, or NULL): a
+ * per-q-head logit that joins every row's softmax with value 0, as
+ * ragged_paged_attention_hd64's attention_sink does
+ *   src/vllm_torchtpu/kernels/ragged_paged_attention/v3/kernel_hd64.py:1377-1388,
+ *   reference semantics :161-172.
+ * lse as in rpa_forward_lse; lse and attention_sink together are
+ * RPA_ERR_UNSUPPORTED.  The head_dim 64 packed cache of kernel_hd64.py
+ * (:246-261, K|V of a head in one 128-wide row) is described by head_dim = 64,
+ * head_dim_padded = 64 and kv_heads_x2 = 2 * align(num_kv_heads, kv_packing):
+ * the same bytes. */
+int rpa_forward_ex(const rpa_desc* d, const void* queries, const void* keys,
+                   const void* values, void* kv_cache, const int32_t* kv_lens,
+                   const int32_t* page_indices, const int32_t* cu_q_lens,
+                   const int32_t* distribution, void* out, const float* attention_sink,
+                   float* lse, void* workspace, size_t workspace_bytes, void* stream);
 
 /* LSE-weighted merge of num_parts partial attentions of the same rows:
  * outs [num_parts, rows, head_dim] and lses [num_parts, rows] (f32, natural

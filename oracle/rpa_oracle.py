@@ -73,6 +73,11 @@ __all__ = [
     "static_validate_inputs",
     "dynamic_validate_inputs",
     "ref_ragged_paged_attention",
+    "merge_attn_results",
+    "merge_attn_states",
+    "get_kv_cache_shape_hd64",
+    "merge_kv_hd64",
+    "ref_ragged_paged_attention_hd64",
 ]
 
 
@@ -496,6 +501,129 @@ def merge_attn_states(outs, lses):
     out = (e.unsqueeze(-1) * outs).sum(dim=0) / norm_safe.unsqueeze(-1)
     lse_out = torch.where(m_finite, m + torch.log(norm_safe), m)
     return out, lse_out
+
+
+# --------------------------------------------------------------------------
+# kernel_hd64.py (src/vllm_torchtpu/kernels/ragged_paged_attention/v3/
+# kernel_hd64.py): head_dim 64, K|V of a head packed in one 128-wide row,
+# optional attention sinks.
+# --------------------------------------------------------------------------
+def get_kv_cache_shape_hd64(total_num_pages, page_size, actual_num_kv_heads,
+                            actual_head_dim, kv_dtype):
+    """kernel_hd64.py:246-261."""
+    assert actual_head_dim == 64
+    pack = get_dtype_packing(kv_dtype)
+    return (total_num_pages, page_size, align_to(actual_num_kv_heads, pack) // pack,
+            pack, 128)
+
+
+def merge_kv_hd64(k: torch.Tensor, v: torch.Tensor) -> torch.Tensor:
+    """Cache records for k/v rows (kernel_hd64.py:1018-1041): head h's row is
+    K_h (64 values) then V_h (64 values); heads are zero-padded to a multiple
+    of the packing.  [T, align(Hkv, pack) / pack, pack, 128]."""
+    assert k.shape == v.shape and k.dtype == v.dtype and k.shape[2] == 64
+    t, hkv, _ = k.shape
+    pack = get_dtype_packing(k.dtype)
+    heads = align_to(hkv, pack)
+    out = torch.zeros((t, heads, 128), dtype=k.dtype)
+    out[:, :hkv] = torch.cat([k, v], dim=-1)
+    return out.reshape(t, heads // pack, pack, 128)
+
+
+def ref_ragged_paged_attention_hd64(
+    queries, keys, values, kv_cache, kv_lens, page_indices, cu_q_lens, distribution,
+    attention_sink=None, *, sm_scale: float = 1.0, sliding_window: int | None = None,
+    soft_cap: float | None = None, mask_value: float | None = None,
+    q_scale: float | None = None, k_scale: float | None = None,
+    v_scale: float | None = None, skip_kv_update: bool = False,
+    use_causal_mask: bool = True, mode: str = "fp32",
+):
+    """CPU restatement of ref_ragged_paged_attention_hd64 (kernel_hd64.py:43-183).
+
+    Returns (out [cu_q_lens[num_seqs], Hq, 64], new_kv_cache).  Per sequence:
+    the cache pages are gathered, the new [K|V] records overlaid at positions
+    [kv_len - q_len, kv_len) and written back (:124-136); logits q . k scaled
+    by sm_scale, k_scale, q_scale (:147-152), soft cap (:162-163), the mask --
+    causal when use_causal_mask, and the window q_pos - W >= k_pos whether or
+    not causal -- replaced by mask_value (:157-164); with attention_sink, the
+    sink logit of each q head is prepended to every row before the softmax and
+    its column dropped afterwards (:166-172): it adds to the denominator only.
+    `mode`: "fp32"/"fp64" keep every intermediate in that precision (the
+    tolerance target); "faithful" keeps the reference's cast points (f32
+    logits and softmax, probabilities cast to the KV dtype, PV in the KV
+    dtype, then the q dtype, then v_scale).
+    """
+    assert mode in ("faithful", "fp32", "fp64")
+    if mask_value is None:  # kernel_hd64.py:65-66, :36
+        mask_value = -0.7 * float(torch.finfo(torch.float32).max)
+    d = queries.shape[2]
+    assert d == 64
+    hq, hkv = queries.shape[1], keys.shape[1]
+    qpk = hq // hkv
+    _, page_size, heads_per_pack, pack, width = kv_cache.shape
+    assert width == 128
+    heads = heads_per_pack * pack
+    max_num_seqs = kv_lens.shape[0]
+    pps = page_indices.shape[0] // max_num_seqs
+    num_seqs = int(distribution[2])
+    kv_dtype = kv_cache.dtype
+    work = torch.from_numpy(_int_view(kv_cache).copy())
+    merged = torch.from_numpy(_int_view(merge_kv_hd64(keys, values)))
+    acc = {"fp32": torch.float32, "fp64": torch.float64, "faithful": torch.float32}[mode]
+    outputs = []
+    for i in range(num_seqs):
+        q_start, q_end = int(cu_q_lens[i]), int(cu_q_lens[i + 1])
+        q_len = q_end - q_start
+        kv_len = int(kv_lens[i])
+        assert kv_len - q_len >= 0
+        idx = page_indices[i * pps:i * pps + cdiv(kv_len, page_size)].long()
+        gathered = work[idx].reshape(-1, heads_per_pack, pack, 128).clone()
+        if not skip_kv_update:
+            gathered[kv_len - q_len:kv_len] = merged[q_start:q_end]
+            work[idx] = gathered.reshape(-1, page_size, heads_per_pack, pack, 128)
+        kv = gathered.view(kv_dtype).reshape(-1, heads, 128)[:kv_len, :hkv]
+        kv = kv.repeat_interleave(qpk, dim=1)  # [kv_len, Hq, 128]
+        q = queries[q_start:q_end]
+        if q_scale is not None:  # kernel_hd64.py:137-144
+            q = q / q_scale
+            info = torch.finfo(kv_dtype)
+            q = torch.clamp(q, min=info.min, max=info.max).to(kv_dtype)
+        # q padded with 64 zeros meets only the K half of each row (:118, :146).
+        attn = torch.einsum("qhd,khd->hqk", q.to(acc), kv[..., :64].to(acc))
+        attn = attn * sm_scale
+        if k_scale is not None:
+            attn = attn * k_scale
+        if q_scale is not None:
+            attn = attn * q_scale
+        q_pos = (kv_len - q_len) + torch.arange(q_len).view(1, q_len, 1)
+        k_pos = torch.arange(kv_len).view(1, 1, kv_len)
+        mask = (q_pos < k_pos) if use_causal_mask else torch.zeros((1, q_len, kv_len),
+                                                                   dtype=torch.bool)
+        if sliding_window is not None:
+            mask = mask | (q_pos - sliding_window >= k_pos)
+        if soft_cap is not None:
+            attn = soft_cap * torch.tanh(attn / soft_cap)
+        attn = torch.where(mask, torch.tensor(mask_value, dtype=acc), attn)
+        if attention_sink is not None:
+            sink = attention_sink.to(acc).view(hq, 1, 1).expand(hq, q_len, 1)
+            attn = torch.softmax(torch.cat([sink, attn], dim=2), dim=-1)[..., 1:]
+        else:
+            attn = torch.softmax(attn, dim=-1)
+        vals = kv[..., 64:]
+        if mode == "faithful":
+            p = attn.to(kv_dtype).to(torch.float32)
+            out = torch.einsum("hqk,khd->qhd", p, vals.to(torch.float32)).to(kv_dtype)
+            out = out.to(queries.dtype)
+        else:
+            out = torch.einsum("hqk,khd->qhd", attn, vals.to(acc))
+        if v_scale is not None:
+            out = out * v_scale
+        outputs.append(out)
+    if outputs:
+        result = torch.cat(outputs, dim=0)
+    else:
+        result = torch.empty((0, hq, d), dtype=queries.dtype if mode == "faithful" else acc)
+    return result, work.view(kv_dtype)
 
 
 def _self_check():  # pragma: no cover - manual use

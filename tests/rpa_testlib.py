@@ -12,11 +12,14 @@ import torch
 def brute_force_rpa(q, k, v, kv_cache, kv_lens, page_indices, cu_q_lens, distribution, *,
                     sm_scale=1.0, sliding_window=None, soft_cap=None, k_scale=None,
                     v_scale=None, use_causal_mask=True, skip_kv_update=False,
-                    return_lse=False):
+                    return_lse=False, attention_sink=None):
     """Per-element fp64 attention written directly from the semantic contract
     (positions, page table, K/V combined-head interleave), independent of the
     oracle's gather/einsum code.  Returns [num_tokens, Hq, D] float64 (and,
-    with return_lse, the per-row log(sum_j exp(logit_j)) [num_tokens, Hq])."""
+    with return_lse, the per-row log(sum_j exp(logit_j)) [num_tokens, Hq]).
+    attention_sink [Hq]: one more term exp(sink) in each row's denominator.
+    A head_dim 64 packed cache is read through its view
+    [P, ps, 2 * heads / pack, pack, 64] (K_h at combined head 2h, V_h at 2h + 1)."""
     Q = q.to(torch.float64).numpy()
     K = k.to(torch.float64).numpy()
     V = v.to(torch.float64).numpy()
@@ -63,6 +66,8 @@ def brute_force_rpa(q, k, v, kv_cache, kv_lens, page_indices, cu_q_lens, distrib
                 m = max(logits)
                 w = [math.exp(x - m) for x in logits]
                 tot = sum(w)
+                if attention_sink is not None:
+                    tot += math.exp(float(attention_sink[gq]) - m)
                 o = sum(wi * vi for wi, vi in zip(w, vals)) / tot
                 if v_scale is not None:
                     o = o * v_scale
@@ -93,3 +98,18 @@ def bytes_equal(a: torch.Tensor, b: torch.Tensor) -> bool:
     assert a.dtype == b.dtype and a.shape == b.shape
     itype = {1: torch.uint8, 2: torch.int16, 4: torch.int32, 8: torch.int64}[a.element_size()]
     return bool(torch.equal(a.contiguous().view(itype).cpu(), b.contiguous().view(itype).cpu()))
+
+
+def bytes_diff(a: torch.Tensor, b: torch.Tensor, limit: int = 8) -> str:
+    """Where two same-shaped tensors differ bitwise: count and the first
+    `limit` indices with both values (for failure messages)."""
+    itype = {1: torch.uint8, 2: torch.int16, 4: torch.int32, 8: torch.int64}[a.element_size()]
+    ai = a.contiguous().view(itype).cpu()
+    bi = b.contiguous().view(itype).cpu()
+    bad = (ai != bi).nonzero()
+    lines = [f"{bad.shape[0]} of {ai.numel()} elements differ"]
+    for idx in bad[:limit].tolist():
+        t = tuple(idx)
+        lines.append(f"  at {t}: {int(ai[t]) & 0xff:#04x} vs {int(bi[t]) & 0xff:#04x}"
+                     if a.element_size() == 1 else f"  at {t}: {int(ai[t])} vs {int(bi[t])}")
+    return "\n".join(lines)

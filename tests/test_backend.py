@@ -24,6 +24,11 @@ def test_kv_cache_shape_and_page_bytes():
     assert BE.get_kv_cache_shape(10, 16, 8, 128, E5M2) == (10, 16, 4, 4, 128)
     assert BE.get_kv_cache_shape(3, 32, 3, 80, BF16) == (3, 32, 3, 2, 128)
     assert BE.get_kv_cache_shape(3, 32, 1, 256, "fp8_e4m3") == (3, 32, 1, 4, 256)
+    # head_size 64: K|V packed along one 128-wide row (Kx2 = num_kv_heads).
+    assert BE.get_kv_cache_shape(10, 16, 8, 64) == (10, 16, 8, 1, 128)
+    assert BE.get_kv_cache_shape(10, 16, 8, 64, BF16) == (10, 16, 4, 2, 128)
+    assert BE.get_kv_cache_shape(10, 16, 3, 64, "fp8") == (10, 16, 1, 4, 128)
+    assert BE.get_kv_cache_page_size_bytes(16, 8, 64, BF16) == 16 * 8 * 128 * 2
     # one page = block_size records of Kx2 * Dp elements
     assert BE.get_kv_cache_page_size_bytes(16, 8, 128, BF16) == 16 * 16 * 128 * 2
     assert BE.get_kv_cache_page_size_bytes(16, 8, 128, "fp8") == 16 * 16 * 128
@@ -100,11 +105,14 @@ def _run(head_size, pool_heads, pool_head_size, *, kv_cache_dtype="bf16", two_d=
 
 
 def test_forward_query_width_and_layout():
-    # A layer on its own page gets no padding; a head_dim 64 layer on a
-    # head_dim 128 pool has the same page geometry here (see module docstring).
-    for hs, ph, phs in ((128, 4, 128), (64, 4, 64), (64, 4, 128)):
+    # A layer on its own page gets no padding.
+    for hs, ph, phs in ((128, 4, 128), (64, 4, 64)):
         out, _, seen, _, q = _run(hs, ph, phs)
         assert seen["q"].shape[-1] == hs and out.shape == q.shape
+    # A head_dim 64 layer on a head_dim 128 pool page (a wider spec's) is
+    # padded to 128 and goes to the v3 layout (attention.py:215-247).
+    out, _, seen, _, q = _run(64, 4, 128)
+    assert seen["q"].shape[-1] == 128 and out.shape == q.shape
     # A 128-wide layer on a 256-wide pool is padded to 256, then sliced back.
     out, _, seen, _, q = _run(128, 4, 256)
     assert seen["q"].shape == (3, 4, 256) and out.shape == q.shape
@@ -145,3 +153,23 @@ def test_kernel_registry_caches_per_config():
     assert impl._build_rpa_kernel(None, None, None) is a
     assert impl._build_rpa_kernel(None, 0.5, 2.0) is not a
     assert impl._build_rpa_kernel(None, None, None, skip_kv_update=True) is not a
+
+
+def test_sinks_routing():
+    """Sinks are kept (as f32 after loading) and only the head_dim 64 kernel
+    takes them (attention_interface.py:418-436)."""
+    sinks = torch.randn(4).to(BF16)
+    impl = B.RpaAttentionBackendImpl(num_heads=4, head_size=128, scale=1.0, num_kv_heads=2,
+                                     alibi_slopes=None, sliding_window=None,
+                                     kv_cache_dtype="auto", sinks=sinks)
+    impl.process_weights_after_loading(BF16)
+    assert impl.sinks.dtype == torch.float32 and torch.equal(impl.sinks, sinks.float())
+    with pytest.raises(AssertionError):
+        B.RpaAttentionBackendImpl(num_heads=4, head_size=128, scale=1.0, num_kv_heads=2,
+                                  alibi_slopes=None, sliding_window=None,
+                                  kv_cache_dtype="auto", sinks=torch.zeros(3))
+    kernel = impl._build_rpa_kernel(None, None, None)
+    q = torch.zeros(2, 4, 128, dtype=BF16)
+    with pytest.raises(NotImplementedError, match="head_dim==64"):
+        kernel(None, q, q[:, :2], q[:, :2], None, torch.zeros(1, dtype=torch.int32), None,
+               None, impl.sinks)

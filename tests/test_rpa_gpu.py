@@ -142,6 +142,18 @@ def test_complex_shapes(gpu_device, num_seqs, heads, d):
     check(W.make_workload(seqs, heads[0], heads[1], d, 16, seed=5, name="complex"), gpu_device)
 
 
+@pytest.mark.parametrize("d", [128, 256])
+def test_prefill_kernel_writes_without_decode_kernel(gpu_device, d):
+    """qpk > 16 has no decode kernel, so the prefill launch plans the cache
+    writes itself, in 512-thread (d 128) or 256-thread (d 256) workgroups; the
+    first sequences' rows must all be written (their kv_len entries share LDS
+    with the plan's reduction slots)."""
+    seqs = [(17, 80), (1, 300), (64, 64), (5, 18), (1, 33), (40, 41)]
+    for rep in range(3):
+        check(W.make_workload(seqs, 24, 1, d, 16, seed=90 + rep, name=f"no-decode-{rep}"),
+              gpu_device)
+
+
 @pytest.mark.parametrize("window", [None, 5, 128])
 def test_sliding_window(gpu_device, window):
     g = torch.Generator().manual_seed(1234)

@@ -17,6 +17,13 @@ from .rpa import (
     rpa_kv_cache_update,
     static_validate_inputs,
 )
+from .rpa_hd64 import (
+    dynamic_validate_inputs_hd64,
+    get_kv_cache_shape_hd64,
+    merge_kv_hd64,
+    ragged_paged_attention_hd64,
+    static_validate_inputs_hd64,
+)
 from .util import align_to, cdiv, get_dtype_packing, next_power_of_2
 
 __all__ = [
@@ -24,16 +31,21 @@ __all__ = [
     "align_to",
     "cdiv",
     "dynamic_validate_inputs",
+    "dynamic_validate_inputs_hd64",
     "get_dtype_packing",
     "get_kv_cache_shape",
+    "get_kv_cache_shape_hd64",
     "merge_attn_results",
     "merge_attn_states",
     "merge_kv",
+    "merge_kv_hd64",
     "next_power_of_2",
     "quantize_kv",
     "ragged_paged_attention",
     "ragged_paged_attention_bundled",
+    "ragged_paged_attention_hd64",
     "rpa_kv_cache_update",
     "static_per_tensor_quantize_tensor",
     "static_validate_inputs",
+    "static_validate_inputs_hd64",
 ]

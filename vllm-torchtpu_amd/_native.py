@@ -54,6 +54,7 @@ EXPORTED_SYMBOLS = (
     "rpa_kv_cache_update",
     "rpa_forward",
     "rpa_forward_lse",
+    "rpa_forward_ex",
     "rpa_merge_attn_states",
 )
 
@@ -126,6 +127,8 @@ def lib() -> ctypes.CDLL:
     L.rpa_forward.argtypes = [desc_p] + [P] * 10 + [ctypes.c_size_t, P]
     L.rpa_forward_lse.restype = ctypes.c_int
     L.rpa_forward_lse.argtypes = [desc_p] + [P] * 11 + [ctypes.c_size_t, P]
+    L.rpa_forward_ex.restype = ctypes.c_int
+    L.rpa_forward_ex.argtypes = [desc_p] + [P] * 12 + [ctypes.c_size_t, P]
     L.rpa_merge_attn_states.restype = ctypes.c_int
     L.rpa_merge_attn_states.argtypes = [ctypes.c_int32, ctypes.c_int64, ctypes.c_int32,
                                         ctypes.c_int32, P, P, P, P, P]

@@ -24,17 +24,17 @@ What is mirrored:
     cached callable per (window, scales, skip_kv_update) so a compiled graph
     reuses it.
 
+Two cache layouts, as in the reference (attention.py:617-656): head_size 64
+uses the packed layout of ragged_paged_attention_hd64 (K|V of a head in one
+128-wide row) and the hd64 kernel, the only one that takes attention sinks
+(layers/core/attention_interface.py:418-436); every other head size uses
+K and V interleaved per head with head_dim padded to a multiple of 128.
+
 Deliberate differences:
-  * One cache layout for every head size: K and V interleaved per head,
-    head_dim padded to a multiple of 128 (kernel.py:278-292).  The reference
-    packs head_dim 64 as K|V along one 128-wide row; here a head_dim 64 layer
-    uses the padded layout, so it writes into a head_dim 128 pool without
-    extra q/k/v padding (the page geometry is the same).
   * `get_max_num_seqs*` report the batch the fused kernels plan in LDS
     (2048 sequences); the reference's figure is a TPU SMEM budget.
-  * Attention sinks, DCP/PCP sharding and the bundled (block-major) pool are
-    not routed here (the bundled cache has its own entry point,
-    `ragged_paged_attention_bundled`).
+  * DCP/PCP sharding and the bundled (block-major) pool are not routed here
+    (the bundled cache has its own entry point, `ragged_paged_attention_bundled`).
 """
 
 from __future__ import annotations
@@ -46,6 +46,7 @@ from typing import Any
 import torch
 
 from . import rpa as _rpa
+from . import rpa_hd64 as _rpa_hd64
 from .quantization import quantize_kv
 from .util import cdiv, next_power_of_2
 
@@ -126,13 +127,20 @@ class RpaAttentionBackend:
     def get_kv_cache_shape(num_blocks: int, block_size: int, num_kv_heads: int,
                            head_size: int,
                            cache_dtype_str: str | torch.dtype = "auto") -> tuple[int, ...]:
-        """[num_blocks, block_size, Kx2 / packing, packing, padded head size].
-        With "auto" (vLLM's offloading probe, which only looks for num_blocks
-        at dim 0) the packing is left at 1, as the reference does."""
+        """[num_blocks, block_size, Kx2 / packing, packing, padded head size],
+        Kx2 = num_kv_heads for head_size 64 (K|V packed along the row) and
+        2 * num_kv_heads otherwise.  With "auto" (vLLM's offloading probe,
+        which only looks for num_blocks at dim 0) the packing is left at 1, as
+        the reference does."""
         padded = cdiv(head_size, HEAD_SIZE_ALIGNMENT) * HEAD_SIZE_ALIGNMENT
+        use_hd64 = head_size == 64
         if isinstance(cache_dtype_str, str) and cache_dtype_str.lower().strip() == "auto":
-            return (num_blocks, block_size, 2 * num_kv_heads, 1, padded)
+            kx2 = num_kv_heads if use_hd64 else 2 * num_kv_heads
+            return (num_blocks, block_size, kx2, 1, padded)
         kv_dtype = resolve_kv_cache_dtype(cache_dtype_str)
+        if use_hd64:
+            return tuple(_rpa_hd64.get_kv_cache_shape_hd64(num_blocks, block_size, num_kv_heads,
+                                                           head_size, kv_dtype))
         return tuple(_rpa.get_kv_cache_shape(num_blocks, block_size, num_kv_heads, head_size,
                                              kv_dtype))
 
@@ -201,14 +209,20 @@ class RpaAttentionBackendImpl:
             raise NotImplementedError(
                 "Encoder self-attention and encoder/decoder cross-attention are not "
                 "implemented for RpaAttentionBackendImpl")
-        if sinks is not None:
-            raise NotImplementedError("Attention sinks are not supported by the RPA kernels.")
+        if sinks is not None:  # attention.py:914-920
+            assert sinks.shape[0] == num_heads, (
+                "Sinks must have the same number of heads as the number of heads in the layer")
+        self.sinks = sinks
         self.kv_cache_quantized_dtype = None
         if is_fp8_kv_cache_dtype(kv_cache_dtype):
             self.kv_cache_quantized_dtype = STR_DTYPE_TO_TORCH_DTYPE[
                 kv_cache_dtype.lower().strip()]
-        self.sinks = None
         self._kernel_config_cache: dict = {}
+
+    def process_weights_after_loading(self, act_dtype: torch.dtype) -> None:
+        """attention.py:1455-1463: the kernels take f32 sinks."""
+        if self.sinks is not None:
+            self.sinks = torch.nn.Parameter(self.sinks.to(torch.float32), requires_grad=False)
 
     def _build_rpa_kernel(self, q_scale: float | None, k_scale: float | None,
                           v_scale: float | None, skip_kv_update: bool = False):
@@ -224,8 +238,21 @@ class RpaAttentionBackendImpl:
 
         def rpa_kernel_impl(kv_cache, query, key_t, value, seq_lens, block_tables,
                             query_start_loc, request_distribution, sink):
+            # head_dim 64 goes to the hd64 kernel, strict window
+            # (attention_interface.py:418-436); only it takes sinks.
+            if query.shape[-1] == 64:
+                out, _ = _rpa_hd64.ragged_paged_attention_hd64(
+                    query, key_t, value, kv_cache, seq_lens, block_tables.reshape(-1),
+                    query_start_loc, request_distribution,
+                    None if sink is None else sink.detach().to(torch.float32).contiguous(),
+                    sm_scale=self.scale, sliding_window=self.sliding_window,
+                    strict_sliding_window=True, soft_cap=self.logits_soft_cap,
+                    q_scale=q_scale, k_scale=k_scale, v_scale=v_scale,
+                    skip_kv_update=skip_kv_update, use_causal_mask=self.use_causal_mask)
+                return out
             if sink is not None:
-                raise NotImplementedError("attention sinks")
+                raise NotImplementedError(
+                    "Attention sink support is only available when head_dim==64")
             out, _ = _rpa.ragged_paged_attention(
                 query, key_t, value, kv_cache, seq_lens, block_tables.reshape(-1),
                 query_start_loc, request_distribution, use_causal_mask=self.use_causal_mask,

@@ -121,8 +121,15 @@ int rpa_validate_desc(const rpa_desc* d) {
   if (d->num_q_heads % d->num_kv_heads != 0) return RPA_ERR_INVALID_ARG;
   const int pack = 4 / kvb;
   if (d->kv_packing != pack) return RPA_ERR_INVALID_ARG;
-  if (d->head_dim_padded != align64(d->head_dim, 128)) return RPA_ERR_INVALID_ARG;
-  if (d->kv_heads_x2 != align64(2LL * d->num_kv_heads, pack)) return RPA_ERR_INVALID_ARG;
+  // Two cache layouts (kernel.py:278-292 and kernel_hd64.py:246-261): heads
+  // packed with head_dim padded to 128, or, for head_dim 64 only, K|V of a
+  // head side by side in one 128-wide row -- the same bytes as head_dim_padded
+  // 64 with kv heads padded to the packing before doubling.
+  const bool hd64_packed = d->head_dim == 64 && d->head_dim_padded == 64;
+  if (!hd64_packed && d->head_dim_padded != align64(d->head_dim, 128)) return RPA_ERR_INVALID_ARG;
+  const int64_t kx2 = hd64_packed ? 2 * align64(d->num_kv_heads, pack)
+                                  : align64(2LL * d->num_kv_heads, pack);
+  if (d->kv_heads_x2 != kx2) return RPA_ERR_INVALID_ARG;
   if (d->page_size <= 0 || d->page_size % pack != 0) return RPA_ERR_INVALID_ARG;
   if (d->total_num_pages <= 0 || d->max_num_tokens < 0) return RPA_ERR_INVALID_ARG;
   if (d->max_num_seqs <= 0 || d->pages_per_seq < 0) return RPA_ERR_INVALID_ARG;
@@ -168,14 +175,23 @@ int rpa_forward(const rpa_desc* d, const void* queries, const void* keys, const 
                 void* kv_cache, const int32_t* kv_lens, const int32_t* page_indices,
                 const int32_t* cu_q_lens, const int32_t* distribution, void* out,
                 void* workspace, size_t workspace_bytes, void* stream) {
-  return rpa_forward_lse(d, queries, keys, values, kv_cache, kv_lens, page_indices, cu_q_lens,
-                         distribution, out, nullptr, workspace, workspace_bytes, stream);
+  return rpa_forward_ex(d, queries, keys, values, kv_cache, kv_lens, page_indices, cu_q_lens,
+                        distribution, out, nullptr, nullptr, workspace, workspace_bytes, stream);
 }
 
 int rpa_forward_lse(const rpa_desc* d, const void* queries, const void* keys, const void* values,
                     void* kv_cache, const int32_t* kv_lens, const int32_t* page_indices,
                     const int32_t* cu_q_lens, const int32_t* distribution, void* out, float* lse,
                     void* workspace, size_t workspace_bytes, void* stream) {
+  return rpa_forward_ex(d, queries, keys, values, kv_cache, kv_lens, page_indices, cu_q_lens,
+                        distribution, out, nullptr, lse, workspace, workspace_bytes, stream);
+}
+
+int rpa_forward_ex(const rpa_desc* d, const void* queries, const void* keys, const void* values,
+                   void* kv_cache, const int32_t* kv_lens, const int32_t* page_indices,
+                   const int32_t* cu_q_lens, const int32_t* distribution, void* out,
+                   const float* attention_sink, float* lse, void* workspace,
+                   size_t workspace_bytes, void* stream) {
   const int st = rpa_validate_desc(d);
   if (st != RPA_OK) return st;
   if (d->max_num_tokens == 0) return RPA_OK;
@@ -188,9 +204,13 @@ int rpa_forward_lse(const rpa_desc* d, const void* queries, const void* keys, co
                           reinterpret_cast<uintptr_t>(out) | reinterpret_cast<uintptr_t>(keys) |
                           reinterpret_cast<uintptr_t>(values);
   if (align & 15u) return RPA_ERR_INVALID_ARG;
+  // An LSE over keys with a sink folded in would count the sink once per
+  // merged partial; the reference has no such output either.
+  if (lse != nullptr && attention_sink != nullptr) return RPA_ERR_UNSUPPORTED;
   hipStream_t s = static_cast<hipStream_t>(stream);
   rpa::Params p = make_params(d);
   p.lse = lse;
+  p.sink = attention_sink;
   const bool decode_only = d->path == RPA_PATH_DECODE_ONLY;
   if (decode_only && !use_decode_kernel(d, p)) return RPA_ERR_UNSUPPORTED;
   if (!use_fused_path(d, p)) {

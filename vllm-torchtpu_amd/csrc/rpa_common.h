@@ -37,6 +37,7 @@ struct Params {
   int32_t decode_waves;    // wavefronts of the decode kernel's persistent grid (0: no decode kernel)
   int32_t prefill_on;      // the prefill kernel attends the non-decode rows
   float* lse;              // [T, Hq] natural-log LSE of each output row, or null
+  const float* sink;       // [Hq] attention-sink logits (natural log), or null
 };
 
 constexpr float kLn2 = 0.6931471805599453f;
@@ -47,6 +48,15 @@ constexpr float kLn2 = 0.6931471805599453f;
 // m = -inf gives (batched_rpa/kernel.py:116-124).
 __device__ __forceinline__ float lse_from_log2(float m, float l) {
   return l > 0.0f ? (m + __log2f(l)) * kLn2 : -INFINITY;
+}
+
+// Row sum with q head g's attention sink (kernel_hd64.py:161-172, :450-456):
+// the sink is one more logit in the softmax, with value 0, so it adds
+// 2^(sink log2 e - m) to the sum l of 2^(s - m) (m: the row's reference max,
+// log2 units).  A sink far above m sends the sum to +inf and the row to 0.
+__device__ __forceinline__ float sum_with_sink(const Params& p, int32_t g, float m, float l) {
+  if (p.sink == nullptr) return l;
+  return l + exp2f(p.sink[g] * 1.4426950408889634f - m);
 }
 
 // Page and slot of logical position j (>= 0): shifts for power-of-two page

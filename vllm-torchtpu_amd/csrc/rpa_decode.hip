@@ -479,7 +479,8 @@ decode_kernel(Params p, const uint16_t* __restrict__ q, const typename KV::stora
       const int32_t s = cur.s, h = cur.h;
       if (last_tile && cur.lt0 == 0) {
         if (n < rows) {
-          const float inv = (lsum == 0.0f) ? 0.0f : p.v_scale / lsum;
+          const float lsum_s = sum_with_sink(p, h * p.qpk + n, m_run, lsum);
+          const float inv = lsum_s > 0.0f ? p.v_scale / lsum_s : 0.0f;
           const int64_t orow_i = static_cast<int64_t>(tq_cur) * p.Hq + h * p.qpk + n;
           if (p.lse != nullptr && g == 0) p.lse[orow_i] = lse_from_log2(m_run, lsum);
           OutS* orow = out + orow_i * p.D;
@@ -543,6 +544,12 @@ hipError_t launch_dp(const Params& p, const DecodeWorkspace& ws, const void* q, 
                      const void* v, void* cache, const int32_t* kv_lens,
                      const int32_t* page_indices, const int32_t* cu, const int32_t* dist,
                      void* out, hipStream_t stream) {
+  if (p.Dp == 64) {
+    // A 128-byte load part holds K (or V) of one token only for 2-byte elements.
+    if constexpr (sizeof(typename KV::storage) == 2)
+      return launch_typed<KV, 64, OutS>(p, ws, q, k, v, cache, kv_lens, page_indices, cu, dist, out, stream);
+    return hipErrorInvalidValue;
+  }
   if (p.Dp == 128)
     return launch_typed<KV, 128, OutS>(p, ws, q, k, v, cache, kv_lens, page_indices, cu, dist, out, stream);
   if (p.Dp == 256)
@@ -575,7 +582,8 @@ bool decode_supported(const Params& p, int q_dtype, int kv_dtype, int out_dtype)
       kv_dtype != RPA_DTYPE_FP8_E5M2)
     return false;
   if (out_dtype != RPA_DTYPE_BF16 && out_dtype != RPA_DTYPE_F32) return false;
-  if (p.Dp != 128 && p.Dp != 256) return false;
+  if (p.Dp != 64 && p.Dp != 128 && p.Dp != 256) return false;
+  if (p.Dp == 64 && kv_dtype != RPA_DTYPE_BF16) return false;
   if (p.D % 8 != 0 || p.qpk > 16) return false;
   if (p.S > kMaxDecodeSeqs) return false;
   // The work line (tiles of every pair) is indexed with 32-bit integers.

@@ -99,7 +99,9 @@ hipError_t launch_dp(const Params& p, const DecodeWorkspace& ws, const void* q, 
                      static_cast<const uint16_t*>(q), static_cast<const E*>(k),                   \
                      static_cast<const E*>(v), static_cast<E*>(cache), kv_lens, page_indices, cu, \
                      dist, static_cast<OutS*>(out), ws.part_o, ws.part_ml, ws.plan)
-  if (p.Dp == 128) {
+  if (p.Dp == 64) {
+    RPA_FINISH_LAUNCH(64);
+  } else if (p.Dp == 128) {
     RPA_FINISH_LAUNCH(128);
   } else if (p.Dp == 256) {
     RPA_FINISH_LAUNCH(256);
@@ -135,7 +137,7 @@ bool finish_supported(const Params& p, int q_dtype, int kv_dtype, int out_dtype)
       kv_dtype != RPA_DTYPE_FP8_E5M2)
     return false;
   if (out_dtype != RPA_DTYPE_BF16 && out_dtype != RPA_DTYPE_F32) return false;
-  if (p.Dp != 128 && p.Dp != 256) return false;
+  if (p.Dp != 64 && p.Dp != 128 && p.Dp != 256) return false;
   if (p.D % 8 != 0 || p.S > kMaxDecodeSeqs) return false;
   return true;
 }

@@ -113,7 +113,9 @@ __device__ __forceinline__ void generic_row(const Params& p, const float* qs,
     }
   }
 
-  const float inv_l = (l_run == 0.0f) ? 0.0f : p.v_scale / l_run;
+  // The attention sink (a logit with value 0) joins the sum.
+  const float l_s = p.sink != nullptr ? l_run + __expf(p.sink[g] - m_run) : l_run;
+  const float inv_l = l_s > 0.0f ? p.v_scale / l_s : 0.0f;
   if (p.lse != nullptr && lane == 0)
     p.lse[static_cast<int64_t>(t) * p.Hq + g] = l_run > 0.0f ? m_run + __logf(l_run) : -INFINITY;
   OutS* orow = out + (static_cast<int64_t>(t) * p.Hq + g) * p.D;

@@ -80,8 +80,12 @@ __device__ __forceinline__ void merge_partials(const Params& p, const float* __r
     }
   }
   float scale[RP];
+  const int32_t qh0 = static_cast<int32_t>(orow0 % p.Hq);  // q head of row 0
 #pragma unroll
-  for (int r = 0; r < RP; ++r) scale[r] = (L[r] == 0.0f) ? 0.0f : p.v_scale / L[r];
+  for (int r = 0; r < RP; ++r) {
+    const float ls = r < rows ? sum_with_sink(p, qh0 + r, M[r], L[r]) : L[r];
+    scale[r] = ls > 0.0f ? p.v_scale / ls : 0.0f;
+  }
   if (p.lse != nullptr) {
 #pragma unroll
     for (int r = 0; r < RP; ++r)

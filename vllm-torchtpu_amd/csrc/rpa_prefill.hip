@@ -93,9 +93,9 @@ struct PrefillCfg {
   // head_dim 128: 8 wavefronts (256 q rows), one workgroup per CU with two
   // wavefronts per SIMD -- each K|V tile staged once feeds twice the rows of
   // a 4-wavefront workgroup.  head_dim 256: 4 wavefronts, one per SIMD.
-  static constexpr int THREADS = DP == 128 ? 512 : 256;
+  static constexpr int THREADS = DP <= 128 ? 512 : 256;
   static constexpr int ROWS = 32 * THREADS / 64;   // q rows per item (32 per wavefront)
-  static constexpr int BK = DP == 128 ? 64 : 32;   // keys per tile
+  static constexpr int BK = DP <= 128 ? 64 : 32;   // keys per tile
   static constexpr int NSB = BK / 32;              // 32-key S^T blocks per tile
   // LDS row strides.  K rows (read 16 bytes per lane, 16 consecutive keys
   // per access) are padded by 16 bytes, 4 banks apart; V rows (read with
@@ -174,7 +174,7 @@ __device__ __forceinline__ void prefill_finish_role(
 // Two wavefronts per SIMD at head_dim 128 (256 registers per lane), one at 256.
 // FULL_D: head_dim == Dp (no zero-padded dims to skip).
 template <typename KV, int DP, typename OutS, bool FULL_D>
-__global__ void __launch_bounds__(PrefillCfg<DP>::THREADS) __attribute__((amdgpu_waves_per_eu(DP == 128 ? 2 : 1)))
+__global__ void __launch_bounds__(PrefillCfg<DP>::THREADS) __attribute__((amdgpu_waves_per_eu(DP <= 128 ? 2 : 1)))
 prefill_kernel(Params p, const uint16_t* __restrict__ q,
                const typename KV::storage* __restrict__ keys,
                const typename KV::storage* __restrict__ values,
@@ -531,7 +531,8 @@ prefill_kernel(Params p, const uint16_t* __restrict__ q,
   // ---- output: lane l, block tt, register i -> dim 32tt + 8(i/4) + 4 half + i%4.
   const float lsum = l_run + __shfl_xor(l_run, 32, 64);
   if (!row_ok) return;
-  const float inv = (lsum == 0.0f) ? 0.0f : p.v_scale / lsum;
+  const float lsum_s = sum_with_sink(p, qhead, m_ref, lsum);
+  const float inv = lsum_s > 0.0f ? p.v_scale / lsum_s : 0.0f;
   const int64_t orow_i = static_cast<int64_t>(q_start + tok) * p.Hq + qhead;
   // Lanes l and l + 32 hold the same row.
   if (p.lse != nullptr && half == 0) p.lse[orow_i] = lse_from_log2(m_ref, lsum);
@@ -564,7 +565,7 @@ hipError_t launch_dp(const Params& p, const void* q, const void* k, const void* 
   using E = typename KV::storage;
   // Upper bound on attention items: every sequence adds at most one partial
   // block.
-  const int32_t bq = (p.Dp == 128 ? PrefillCfg<128>::ROWS : PrefillCfg<256>::ROWS) / p.qpk;
+  const int32_t bq = (p.Dp <= 128 ? PrefillCfg<128>::ROWS : PrefillCfg<256>::ROWS) / p.qpk;
   const int64_t blocks = (static_cast<int64_t>(p.T) + bq - 1) / bq + p.S;
   const int32_t nfm = prefill_merge_blocks(p, num_cus);
   const int32_t nfw = prefill_write_blocks(p, num_cus);
@@ -579,7 +580,9 @@ hipError_t launch_dp(const Params& p, const void* q, const void* k, const void* 
                      page_indices, cu, dist, static_cast<OutS*>(out), ws.plan, ws.part_o,    \
                      ws.part_ml, nfm, nfw)
   const bool full = p.D == p.Dp;
-  if (p.Dp == 128) {
+  if (p.Dp == 64) {
+    if (full) RPA_PREFILL_LAUNCH(64, true); else RPA_PREFILL_LAUNCH(64, false);
+  } else if (p.Dp == 128) {
     if (full) RPA_PREFILL_LAUNCH(128, true); else RPA_PREFILL_LAUNCH(128, false);
   } else if (p.Dp == 256) {
     if (full) RPA_PREFILL_LAUNCH(256, true); else RPA_PREFILL_LAUNCH(256, false);
@@ -615,9 +618,9 @@ bool prefill_supported(const Params& p, int q_dtype, int kv_dtype, int out_dtype
       kv_dtype != RPA_DTYPE_FP8_E5M2)
     return false;
   if (out_dtype != RPA_DTYPE_BF16 && out_dtype != RPA_DTYPE_F32) return false;
-  if (p.Dp != 128 && p.Dp != 256) return false;
+  if (p.Dp != 64 && p.Dp != 128 && p.Dp != 256) return false;
   // 8-element pieces of q / k / v rows; at least one query token per item.
-  if (p.D % 8 != 0 || p.qpk > (p.Dp == 128 ? PrefillCfg<128>::ROWS : PrefillCfg<256>::ROWS))
+  if (p.D % 8 != 0 || p.qpk > (p.Dp <= 128 ? PrefillCfg<128>::ROWS : PrefillCfg<256>::ROWS))
     return false;
   if (p.S > kMaxDecodeSeqs) return false;
   return true;

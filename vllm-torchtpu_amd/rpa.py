@@ -292,7 +292,7 @@ def _workspace(device: torch.device, nbytes: int) -> torch.Tensor:
 def _rpa_forward_impl(queries, keys, values, kv_cache, kv_lens, page_indices, cu_q_lens,
                       distribution, out, *, use_causal_mask, skip_kv_update, sm_scale,
                       sliding_window, soft_cap, q_scale, k_scale, v_scale,
-                      path=N.RPA_PATH_AUTO, workspace=None, lse=None):
+                      path=N.RPA_PATH_AUTO, workspace=None, lse=None, attention_sink=None):
     L = N.lib()
     _require_device(queries, keys, values, kv_cache, kv_lens, page_indices, cu_q_lens,
                     distribution, out)
@@ -314,20 +314,21 @@ def _rpa_forward_impl(queries, keys, values, kv_cache, kv_lens, page_indices, cu
         elif workspace.numel() < ws_bytes:
             raise ValueError(f"workspace has {workspace.numel()} bytes, needs {ws_bytes}")
         stream = torch.cuda.current_stream(queries.device).cuda_stream
-        if lse is None:
-            code = L.rpa_forward(desc, _ptr(queries), _ptr(keys), _ptr(values), _ptr(kv_cache),
-                                 _ptr(kv_lens), _ptr(page_indices), _ptr(cu_q_lens),
-                                 _ptr(distribution), _ptr(out), _ptr(workspace),
-                                 ws_bytes, stream)
-        else:
-            if (lse.dtype != torch.float32 or not lse.is_contiguous() or lse.device != out.device
-                    or tuple(lse.shape) != tuple(queries.shape[:2])):
-                raise ValueError(f"lse must be a contiguous f32 {tuple(queries.shape[:2])} "
-                                 f"tensor on {out.device}")
-            code = L.rpa_forward_lse(desc, _ptr(queries), _ptr(keys), _ptr(values),
-                                     _ptr(kv_cache), _ptr(kv_lens), _ptr(page_indices),
-                                     _ptr(cu_q_lens), _ptr(distribution), _ptr(out), _ptr(lse),
-                                     _ptr(workspace), ws_bytes, stream)
+        if lse is not None and (lse.dtype != torch.float32 or not lse.is_contiguous()
+                                or lse.device != out.device
+                                or tuple(lse.shape) != tuple(queries.shape[:2])):
+            raise ValueError(f"lse must be a contiguous f32 {tuple(queries.shape[:2])} "
+                             f"tensor on {out.device}")
+        if attention_sink is not None and (
+                attention_sink.dtype != torch.float32 or not attention_sink.is_contiguous()
+                or attention_sink.device != out.device
+                or tuple(attention_sink.shape) != (queries.shape[1],)):
+            raise ValueError(f"attention_sink must be a contiguous f32 ({queries.shape[1]},) "
+                             f"tensor on {out.device}")
+        code = L.rpa_forward_ex(desc, _ptr(queries), _ptr(keys), _ptr(values), _ptr(kv_cache),
+                                _ptr(kv_lens), _ptr(page_indices), _ptr(cu_q_lens),
+                                _ptr(distribution), _ptr(out), _ptr(attention_sink), _ptr(lse),
+                                _ptr(workspace), ws_bytes, stream)
     N.check(code, "rpa_forward")
     return out
 

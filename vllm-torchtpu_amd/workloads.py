@@ -17,6 +17,7 @@ import torch
 from .quantization import quantize_kv
 from .util import cdiv, get_dtype_packing
 from .rpa import get_kv_cache_shape
+from .rpa_hd64 import get_kv_cache_shape_hd64
 
 
 @dataclasses.dataclass
@@ -59,7 +60,7 @@ def make_workload(seq_lens, num_q_heads, num_kv_heads, head_dim, page_size, *,
                   num_pages=None, pool_factor=1.25, max_num_seqs=None,
                   max_num_tokens=None, pages_per_seq=None, distribution=None,
                   k_scale=None, v_scale=None, nan_fill=False, name="custom",
-                  **kwargs) -> Workload:
+                  layout="v3", **kwargs) -> Workload:
     """Build one ragged batch.
 
     seq_lens: list of (q_len, kv_len).  Each sequence takes cdiv(kv_len, ps)
@@ -67,7 +68,8 @@ def make_workload(seq_lens, num_q_heads, num_kv_heads, head_dim, page_size, *,
     N(0,1) values (quantised with k_scale/v_scale for fp8) everywhere; with
     nan_fill, every cache row, page and page-table slot no sequence uses is
     NaN (or -1 for the table), as the reference's poison tests do
-    (correctness_test.py:280-323).
+    (correctness_test.py:280-323).  layout "hd64" builds the head_dim 64
+    packed cache of ragged_paged_attention_hd64 (K|V of a head in one row).
     """
     g = torch.Generator().manual_seed(seed)
     n = len(seq_lens)
@@ -95,9 +97,20 @@ def make_workload(seq_lens, num_q_heads, num_kv_heads, head_dim, page_size, *,
     else:
         k, v = kf.to(kv_dtype), vf.to(kv_dtype)
 
-    shape = get_kv_cache_shape(num_pages, page_size, num_kv_heads, head_dim, kv_dtype)
+    hd64 = layout == "hd64"
+    assert layout in ("v3", "hd64") and (not hd64 or head_dim == 64)
+    if hd64:
+        shape = get_kv_cache_shape_hd64(num_pages, page_size, num_kv_heads, head_dim, kv_dtype)
+    else:
+        shape = get_kv_cache_shape(num_pages, page_size, num_kv_heads, head_dim, kv_dtype)
     cache_f = randn(*shape)
-    if kv_is_fp8:
+    if kv_is_fp8 and hd64:
+        # K halves of each row with k_scale, V halves with v_scale.
+        half = torch.arange(128).view(1, 1, 1, 1, 128) >= 64
+        scale = torch.where(half, torch.tensor(v_scale or 1.0), torch.tensor(k_scale or 1.0))
+        info = torch.finfo(kv_dtype)
+        kv_cache = torch.clamp(cache_f / scale, info.min, info.max).to(kv_dtype)
+    elif kv_is_fp8:
         # K rows (even combined heads) with k_scale, V rows with v_scale.
         pack = shape[3]
         c = torch.arange(shape[2] * pack).view(shape[2], pack)
