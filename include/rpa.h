@@ -106,7 +106,13 @@ typedef struct rpa_desc {
   float k_scale; /* multiplies the logits; 1.0 when None */
   float v_scale; /* multiplies the output; 1.0 when None */
   int32_t path;  /* rpa_path */
-  int32_t reserved[7];
+  /* Largest q_len of a decode row group (spec-verify windows of K + 1 query
+   * tokens), as batched_rpa/wrapper.py:549 `decode_query_size`; 0 or 1 = one
+   * token.  Sequences with 1 <= q_len <= min(decode_query_size,
+   * 16 / (num_q_heads / num_kv_heads)) run on the decode kernel; the result
+   * does not depend on it. */
+  int32_t decode_query_size;
+  int32_t reserved[6];
 } rpa_desc;
 
 /* ABI version compiled into the library. */

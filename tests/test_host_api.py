@@ -43,9 +43,9 @@ def test_desc_layout_matches_c():
     #include <stddef.h>
     #include "rpa.h"
     int main(void) {
-      printf("%zu %zu %zu %zu %zu\n", sizeof(rpa_desc), offsetof(rpa_desc, soft_cap),
+      printf("%zu %zu %zu %zu %zu %zu\n", sizeof(rpa_desc), offsetof(rpa_desc, soft_cap),
              offsetof(rpa_desc, sm_scale), offsetof(rpa_desc, path),
-             offsetof(rpa_desc, reserved));
+             offsetof(rpa_desc, decode_query_size), offsetof(rpa_desc, reserved));
       return 0;
     }
     """
@@ -57,7 +57,7 @@ def test_desc_layout_matches_c():
         vals = [int(x) for x in subprocess.check_output([exe]).split()]
     D = N.RpaDesc
     assert vals == [__import__("ctypes").sizeof(D), D.soft_cap.offset, D.sm_scale.offset,
-                    D.path.offset, D.reserved.offset]
+                    D.path.offset, D.decode_query_size.offset, D.reserved.offset]
 
 
 def _desc(**over):
@@ -81,6 +81,7 @@ def test_validate_desc_codes():
     assert L.rpa_validate_desc(_desc(has_soft_cap=1, soft_cap=0.0)) == N.RPA_ERR_INVALID_ARG
     assert L.rpa_validate_desc(_desc(kv_dtype=N.RPA_DTYPE_F16, q_dtype=N.RPA_DTYPE_F16)) in (
         N.RPA_ERR_INVALID_ARG, N.RPA_ERR_UNSUPPORTED)
+    assert L.rpa_validate_desc(_desc(decode_query_size=-1)) == N.RPA_ERR_INVALID_ARG
     assert L.rpa_workspace_size(_desc()) > 0
     assert L.rpa_workspace_size(_desc(abi_version=99)) == 0
     with pytest.raises(ValueError):
@@ -115,11 +116,16 @@ def test_mask_value_policy():
 def test_custom_op_fake_shape():
     from torch._subclasses.fake_tensor import FakeTensorMode
     w = R.workloads.make_workload([(3, 20), (1, 9)], 8, 2, 128, 16, seed=0)
+    W64 = R.workloads.make_workload([(3, 20), (1, 9)], 8, 2, 64, 16, seed=0, layout="hd64")
     with FakeTensorMode() as mode:
         args = [mode.from_tensor(t) for t in w.args()]
         out = torch.ops.rpa_amd.ragged_paged_attention(
-            *args, torch.bfloat16, True, False, 0.1, 0, 0.0, False, 1.0, 1.0, 1.0, 0)
+            *args, torch.bfloat16, True, False, 0.1, 0, 0.0, False, 1.0, 1.0, 1.0, 0, 4)
+        s = torch.ops.rpa_amd.ragged_paged_attention_hd64(
+            *[mode.from_tensor(t) for t in W64.args()], None, True, False, 0.1, 0, 0.0, False,
+            1.0, 1.0, 1.0)
     assert tuple(out.shape) == tuple(w.q.shape) and out.dtype == torch.bfloat16
+    assert tuple(s.shape) == tuple(W64.q.shape)
 
 
 def test_rpa_case_ranges():

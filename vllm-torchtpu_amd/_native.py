@@ -88,7 +88,8 @@ class RpaDesc(ctypes.Structure):
         ("k_scale", ctypes.c_float),
         ("v_scale", ctypes.c_float),
         ("path", ctypes.c_int32),
-        ("reserved", ctypes.c_int32 * 7),
+        ("decode_query_size", ctypes.c_int32),
+        ("reserved", ctypes.c_int32 * 6),
     ]
 
 

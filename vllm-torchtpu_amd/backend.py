@@ -21,8 +21,10 @@ What is mirrored:
     quantize-on-write with the layer's k/v scales (:1560-1569), the output
     buffer written in place, the profiling call with an empty cache;
   * the per-configuration kernel registry (`_build_rpa_kernel`, :971-1193): one
-    cached callable per (window, scales, skip_kv_update) so a compiled graph
-    reuses it.
+    cached callable per (window, scales, skip_kv_update, decode_query_size) so
+    a compiled graph reuses it;
+  * `decode_query_size` (K + 1 query tokens per decode sequence under
+    speculative decoding, :1706-1712), here a constructor keyword.
 
 Two cache layouts, as in the reference (attention.py:617-656): head_size 64
 uses the packed layout of ragged_paged_attention_hd64 (K|V of a head in one
@@ -203,6 +205,12 @@ class RpaAttentionBackendImpl:
         self.logits_soft_cap = logits_soft_cap
         self.kv_sharing_target_layer_name = kv_sharing_target_layer_name
         self.use_causal_mask = kwargs.get("use_causal_mask", True)
+        # Query tokens of a decode sequence: K + 1 under speculative decoding
+        # (the reference reads speculative_config.num_speculative_tokens,
+        # attention.py:1706-1712; head_dim 64 keeps 1).
+        self.decode_query_size = int(kwargs.get("decode_query_size", 1))
+        if head_size == 64:
+            self.decode_query_size = 1
         if alibi_slopes is not None:
             raise NotImplementedError("Alibi slopes is not supported.")
         if attn_type != DECODER:
@@ -231,7 +239,7 @@ class RpaAttentionBackendImpl:
         query_start_loc, request_distribution, sink) -> output, updating the
         cache in place."""
         key = (self.sliding_window, self.logits_soft_cap, q_scale, k_scale, v_scale,
-               skip_kv_update, self.use_causal_mask)
+               skip_kv_update, self.use_causal_mask, self.decode_query_size)
         fn = self._kernel_config_cache.get(key)
         if fn is not None:
             return fn
@@ -258,7 +266,8 @@ class RpaAttentionBackendImpl:
                 query_start_loc, request_distribution, use_causal_mask=self.use_causal_mask,
                 skip_kv_update=skip_kv_update, sm_scale=self.scale,
                 sliding_window=self.sliding_window, soft_cap=self.logits_soft_cap,
-                q_scale=q_scale, k_scale=k_scale, v_scale=v_scale)
+                q_scale=q_scale, k_scale=k_scale, v_scale=v_scale,
+                decode_query_size=self.decode_query_size)
             return out
 
         self._kernel_config_cache[key] = rpa_kernel_impl

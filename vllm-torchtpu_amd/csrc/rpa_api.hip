@@ -52,6 +52,10 @@ rpa::Params make_params(const rpa_desc* d) {
   for (int sh = 0; sh < 31; ++sh)
     if ((1 << sh) == d->page_size) p.ps_shift = sh;
   p.decode_waves = 0;
+  // Decode row groups: q_len tokens x qpk heads fill at most the 16 MFMA
+  // columns of the decode kernel.
+  const int32_t dq_max = p.qpk > 0 && p.qpk <= 16 ? 16 / p.qpk : 1;
+  p.dq = d->decode_query_size < 1 ? 1 : (d->decode_query_size > dq_max ? dq_max : d->decode_query_size);
   return p;
 }
 
@@ -135,6 +139,7 @@ int rpa_validate_desc(const rpa_desc* d) {
   if (d->max_num_seqs <= 0 || d->pages_per_seq < 0) return RPA_ERR_INVALID_ARG;
   if (d->has_soft_cap && d->soft_cap == 0.0f) return RPA_ERR_INVALID_ARG;
   if (d->sliding_window < 0) return RPA_ERR_INVALID_ARG;
+  if (d->decode_query_size < 0) return RPA_ERR_INVALID_ARG;
   if (d->path < RPA_PATH_AUTO || d->path > RPA_PATH_DECODE_ONLY) return RPA_ERR_INVALID_ARG;
   // Implemented combinations.
   if (d->kv_dtype == RPA_DTYPE_F16 || d->q_dtype == RPA_DTYPE_F16) return RPA_ERR_UNSUPPORTED;

@@ -1,4 +1,4 @@
-// Decode attention (one query token per sequence) for gfx950.
+// Decode attention (q_len <= dq query tokens per sequence) for gfx950.
 //
 // Bandwidth-bound GQA split-K with a stream-K split (rpa_plan.h): the tiles
 // of every (decode sequence, kv head) pair lie on one line, pair-major, and
@@ -12,10 +12,11 @@
 // offset of consecutive pairs -- the kv heads of the same tokens, adjacent
 // bytes of the same pages.
 //
-// New tokens.  The key at position kv_len - 1 of a decode row is its own new
-// token: unless skip_kv_update, the wavefront that owns the sequence's last
-// tile reads it from the k/v inputs (patched into its LDS tile) and writes
-// its K|V bytes for that kv head into the cache page (kernel.py:154-166).
+// New tokens.  The keys at positions [kv_len - q_len, kv_len) of a decode
+// sequence are its own new tokens: unless skip_kv_update, the wavefront that
+// owns a tile holding some of them reads them from the k/v inputs (patched
+// into its LDS tile) and writes their K|V bytes for that kv head into the
+// cache pages (kernel.py:154-166).
 //
 // Memory path.  Each global load instruction moves 8 tokens x 128 bytes of
 // one kv head (whole cache lines); a tile is 16 KiB of one head's K|V bytes,
@@ -29,15 +30,18 @@
 // Per 16-token group of a tile a wavefront computes
 //   S^T[token, row] = K[token, :] . Q^T[:, row]      (16x16x32, A = K, B = Q^T)
 //   O^T[dim, row]  += V^T[dim, token] . P^T[token, row] (16x16x16, A = V^T, B = P^T)
-// where the 16 MFMA columns ("rows") are the q heads of this kv head,
-// replicated when q_heads_per_kv_head < 16.  Lane l owns row l % 16 in all
+// where the 16 MFMA columns ("rows") are the (token, q head) pairs of this kv
+// head: column n is token n / qpk of the sequence's q_len (spec-verify windows
+// of several tokens, batched_rpa/wrapper.py:549 decode_query_size) and q head
+// n % qpk; columns past q_len * qpk repeat the last token and are not output.  Lane l owns row l % 16 in all
 // three accumulators, so the online softmax needs two cross-lane shuffles per
 // tile and P feeds the PV product with no shuffle.
 //
-// Semantics match ref_ragged_paged_attention (kernel.py:185-209) for
-// q_len == 1: s_j = (q . k_j) * sm_scale * k_scale * q_scale, optional soft
-// cap, keys j < kv_len (and j >= kv_len - W under a causal window), softmax,
-// out = P . V * v_scale.  P is rounded to bf16 for the PV product, as the
+// Semantics match ref_ragged_paged_attention (kernel.py:185-209):
+// s_j = (q . k_j) * sm_scale * k_scale * q_scale, optional soft cap; token i
+// of q_len at position p_i = kv_len - q_len + i attends keys j <= p_i (all
+// j < kv_len without the causal mask) and j > p_i - W under a causal window;
+// softmax, out = P . V * v_scale.  P is rounded to bf16 for the PV product, as the
 // Pallas kernel does (kernel.py:553); everything else accumulates in fp32.
 #include "rpa_common.h"
 #include "rpa_internal.h"
@@ -133,37 +137,42 @@ struct TileInfo {
   int32_t nt;   // tiles of the pair
   int32_t lo;   // first key of the sequence's range
   int32_t hi;   // end of the sequence's range (kv_len)
+  int32_t ql;   // q_len of the sequence (its new tokens are keys [hi - ql, hi))
 };
 
 __device__ __forceinline__ int32_t uni(int32_t x) { return __builtin_amdgcn_readfirstlane(x); }
 
-// Last tile of a sequence, LDS rows of stride RS bytes (bf16).  Row rn holds
-// key hi - 1, the new token: with `src` it is replaced by the k/v input row.
-// Rows past it (keys >= hi; the loads clamped them to copies of key hi - 1)
-// are zeroed when `zero_tail`, so that their P = 0 never meets a NaN.
-template <typename KV, int DP, int TT>
-__device__ __forceinline__ void patch_last_tile(unsigned char* buf, int rs, int32_t rn,
-                                                const typename KV::storage* src, int32_t D,
-                                                bool zero_tail, int lane) {
+// LDS tile rows of stride RS bytes (bf16).  Rows [r0, r1) hold new tokens:
+// row r0 + k is replaced by the k/v input row src + k * src_stride.
+template <typename KV, int DP>
+__device__ __forceinline__ void patch_rows(unsigned char* buf, int rs, int32_t r0, int32_t r1,
+                                           const typename KV::storage* src, int64_t src_stride,
+                                           int32_t D, int lane) {
   constexpr int PIECES = DP / 8;  // 16-byte bf16 pieces per row
-  if (src != nullptr && lane < PIECES) {
-    const int e0 = lane * 8;
+  for (int32_t i = lane; i < (r1 - r0) * PIECES; i += 64) {
+    const int32_t k = i / PIECES, e0 = (i - k * PIECES) * 8;
     uint4 v = make_uint4(0u, 0u, 0u, 0u);
-    if (e0 < D) v = KV::to_bf16(KV::load8(src + e0));  // D % 8 == 0
-    *reinterpret_cast<uint4*>(buf + rn * rs + 2 * e0) = v;
-  }
-  if (zero_tail) {
-    const int32_t nrows = TT - 1 - rn;
-    for (int32_t i = lane; i < nrows * PIECES; i += 64) {
-      const int32_t r = rn + 1 + i / PIECES, pc = i % PIECES;
-      *reinterpret_cast<uint4*>(buf + r * rs + 16 * pc) = make_uint4(0u, 0u, 0u, 0u);
-    }
+    if (e0 < D) v = KV::to_bf16(KV::load8(src + k * src_stride + e0));  // D % 8 == 0
+    *reinterpret_cast<uint4*>(buf + (r0 + k) * rs + 2 * e0) = v;
   }
 }
 
-// Cache write of a decode row's new token for kv head h (kernel.py:154-166):
-// combined heads 2h (K) and 2h + 1 (V), head dims >= D zero; the wavefront of
-// the last kv head also zeroes the padding heads [2 Hkv, Kx2).
+// Rows [r0, TT) of a sequence's last tile (keys >= kv_len; the loads clamped
+// them to copies of key kv_len - 1) are zeroed, so that their P = 0 never
+// meets a NaN.
+template <int DP, int TT>
+__device__ __forceinline__ void zero_rows(unsigned char* buf, int rs, int32_t r0, int lane) {
+  constexpr int PIECES = DP / 8;
+  for (int32_t i = lane; i < (TT - r0) * PIECES; i += 64) {
+    const int32_t r = r0 + i / PIECES, pc = i % PIECES;
+    *reinterpret_cast<uint4*>(buf + r * rs + 16 * pc) = make_uint4(0u, 0u, 0u, 0u);
+  }
+}
+
+// Cache write of a one-token decode row's new token (position j, input row
+// tq) for kv head h (kernel.py:154-166): combined heads 2h (K) and 2h + 1
+// (V), head dims >= D zero; the wavefront of the last kv head also zeroes the
+// padding heads [2 Hkv, Kx2).
 template <typename KV, int DP>
 __device__ __forceinline__ void write_new_token(const Params& p, typename KV::storage* cache,
                                                 const int32_t* page_indices,
@@ -191,10 +200,47 @@ __device__ __forceinline__ void write_new_token(const Params& p, typename KV::st
   }
 }
 
+// The same for a group's new tokens j0 <= j < j1 (input rows
+// tq0 + j - j0) for kv head h (kernel.py:154-166): combined heads 2h (K) and
+// 2h + 1 (V), head dims >= D zero; the wavefront of the last kv head also
+// zeroes the padding heads [2 Hkv, Kx2).
+template <typename KV, int DP>
+__device__ __forceinline__ void write_new_tokens(const Params& p, typename KV::storage* cache,
+                                                 const int32_t* page_indices,
+                                                 const typename KV::storage* keys,
+                                                 const typename KV::storage* values, int32_t s,
+                                                 int32_t h, int32_t j0, int32_t j1, int32_t tq0,
+                                                 int lane) {
+  using E = typename KV::storage;
+  constexpr int EPP = 8 / sizeof(E);             // elements per 8-byte piece
+  constexpr int PIECES = DP / EPP;               // pieces per head chunk
+  const int32_t npad = h == p.Hkv - 1 ? (p.Kx2 - 2 * p.Hkv) * PIECES : 0;
+  const int32_t per_tok = 2 * PIECES + npad;
+  for (int32_t i = lane; i < (j1 - j0) * per_tok; i += 64) {
+    const int32_t k = i / per_tok, r = i - k * per_tok;
+    const int32_t j = j0 + k;
+    const int32_t pg = page_indices[static_cast<int64_t>(s) * p.pps + page_of(p, j)];
+    if (pg < 0 || pg >= p.P) continue;
+    E* rec = cache + (static_cast<int64_t>(pg) * p.ps + slot_of(p, j)) * p.rec;
+    if (r < 2 * PIECES) {
+      const int c = r / PIECES, e0 = (r - c * PIECES) * EPP;
+      const int64_t src = (static_cast<int64_t>(tq0 + k) * p.Hkv + h) * p.D;
+      uint2 v = make_uint2(0u, 0u);
+      if (e0 < p.D) v = *reinterpret_cast<const uint2*>((c ? values : keys) + src + e0);
+      *reinterpret_cast<uint2*>(rec + static_cast<int64_t>(2 * h + c) * DP + e0) = v;
+    } else {
+      *reinterpret_cast<uint2*>(rec + static_cast<int64_t>(2 * p.Hkv) * DP +
+                                (r - 2 * PIECES) * EPP) = make_uint2(0u, 0u);
+    }
+  }
+}
+
 // ---------------------------------------------------------------------------
 // The decode kernel (one wavefront per SIMD, two tile buffers in flight).
 // ---------------------------------------------------------------------------
-template <typename KV, int DP, typename OutS, bool FULL_D>
+// MULTI: groups of several tokens (dq > 1); without it every group is one
+// token and the per-token bookkeeping folds away.
+template <typename KV, int DP, typename OutS, bool FULL_D, bool MULTI>
 __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1)))
 decode_kernel(Params p, const uint16_t* __restrict__ q, const typename KV::storage* __restrict__ keys,
               const typename KV::storage* __restrict__ values,
@@ -230,8 +276,10 @@ decode_kernel(Params p, const uint16_t* __restrict__ q, const typename KV::stora
   const int32_t g_begin = static_cast<int32_t>(g_begin64);
   const int32_t g_end = min(g_begin + pl.tpw, pl.total_tiles);
   unsigned char* buf = smem + wave * C::WAVE_LDS;
-  const int32_t rows = min(p.qpk, 16);
-  const int32_t rp = decode_slot_rows(p.qpk);
+  const int32_t rp = decode_slot_rows(p.qpk * p.dq);
+  // Column n: token n_tok of the group (clamped to the sequence's q_len), q
+  // head n_head of the kv head.
+  const int32_t n_tok = MULTI ? n / p.qpk : 0;
   const int32_t max_tok = p.pps * p.ps - 1;
   const bool write_kv = p.skip_kv_update == 0;
 
@@ -249,8 +297,9 @@ decode_kernel(Params p, const uint16_t* __restrict__ q, const typename KV::stora
     ti.h = uni(r / ti.nt);
     ti.lt = uni(r - ti.h * ti.nt);
     ti.lt0 = ti.lt;
+    ti.ql = MULTI ? uni(max(L.ql[ti.s], 1)) : 1;
     int32_t lo, hi;
-    decode_range(p, dkv, &lo, &hi);
+    decode_range(p, dkv, ti.ql, &lo, &hi);
     ti.lo = uni(lo);
     ti.hi = uni(hi);
     return ti;
@@ -309,7 +358,7 @@ decode_kernel(Params p, const uint16_t* __restrict__ q, const typename KV::stora
   // (clamped into the row; dims >= head_dim are zeroed where they are used).
   auto load_q = [&](const TileInfo& ti, uint4* qv) __attribute__((always_inline)) {
     const int32_t qh = ti.h * p.qpk + (n % p.qpk);
-    const int32_t tq = L.tq[min(max(ti.s, 0), p.S - 1)];
+    const int32_t tq = L.tq[min(max(ti.s, 0), p.S - 1)] + (MULTI ? min(n_tok, ti.ql - 1) : 0);
     const uint16_t* qrow = q + (static_cast<int64_t>(tq) * p.Hq + qh) * p.D;
 #pragma unroll
     for (int kk = 0; kk < KK; ++kk) {
@@ -353,10 +402,29 @@ decode_kernel(Params p, const uint16_t* __restrict__ q, const typename KV::stora
     const int32_t base = cur.lo + cur.lt * TT;
     const bool last_tile = cur.lt + 1 == cur.nt;
     const int32_t tq_cur = L.tq[cur.s];
+    // This tile's rows [pr0, pr1) are new tokens (keys from new0 on).
+    const int32_t ql = MULTI ? cur.ql : 1;
+    const int32_t new0 = cur.hi - ql;
+    int32_t pr0, pr1;
+    bool patch;
+    if constexpr (MULTI) {
+      pr0 = max(new0 - base, 0);
+      pr1 = min(cur.hi - base, TT);
+      patch = write_kv && pr1 > pr0;
+    } else {
+      pr0 = cur.hi - 1 - base;
+      pr1 = pr0 + 1;
+      patch = write_kv && last_tile;
+    }
+    const int32_t tq_new = tq_cur + base + pr0 - new0;  // input row of row pr0
+    const int64_t new_stride = static_cast<int64_t>(p.Hkv) * p.D;
     const typename KV::storage* knew =
-        keys + (static_cast<int64_t>(tq_cur) * p.Hkv + cur.h) * p.D;
+        keys + (static_cast<int64_t>(tq_new) * p.Hkv + cur.h) * p.D;
     const typename KV::storage* vnew =
-        values + (static_cast<int64_t>(tq_cur) * p.Hkv + cur.h) * p.D;
+        values + (static_cast<int64_t>(tq_new) * p.Hkv + cur.h) * p.D;
+    // Column n's token sits at key position pos; it sees keys [klo, pos].
+    const int32_t pos = p.causal ? new0 + (MULTI ? min(n_tok, ql - 1) : 0) : cur.hi - 1;
+    const int32_t klo = (p.causal && p.window > 0) ? pos - p.window + 1 : 0;
 
     // ---- K: registers -> LDS rows (stride KS) -> MFMA A operand.
     wave_lds_sync();  // the previous tile's V reads are complete
@@ -365,9 +433,9 @@ decode_kernel(Params p, const uint16_t* __restrict__ q, const typename KV::stora
 #pragma unroll
       for (int pt = 0; pt < KP; ++pt)
         store_piece_bf16<KV>(buf + (8 * o + tl) * C::KS, pt * EPP + ol * (EPP / 8), CB[o][pt]);
-    if (last_tile && write_kv) {
+    if (patch) {
       wave_lds_sync();
-      patch_last_tile<KV, DP, TT>(buf, C::KS, cur.hi - 1 - base, knew, p.D, false, lane);
+      patch_rows<KV, DP>(buf, C::KS, pr0, pr1, knew, new_stride, p.D, lane);
     }
     wave_lds_sync();
     f32x4_t sacc[NG];
@@ -408,7 +476,10 @@ decode_kernel(Params p, const uint16_t* __restrict__ q, const typename KV::stora
 #pragma unroll
     for (int i = 0; i < 4 * NG; ++i) {
       const int32_t j = base + 16 * (i >> 2) + 4 * g + (i & 3);
-      sc[i] = (j < cur.hi) ? sc[i] : -INFINITY;
+      if constexpr (MULTI)
+        sc[i] = (j <= pos && j >= klo) ? sc[i] : -INFINITY;
+      else
+        sc[i] = (j < cur.hi) ? sc[i] : -INFINITY;
       tmax = fmaxf(tmax, sc[i]);
     }
     tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
@@ -442,33 +513,43 @@ decode_kernel(Params p, const uint16_t* __restrict__ q, const typename KV::stora
         }
         store_piece_bf16<KV>(buf + (8 * o + tl) * C::VS, (pt - KP) * EPP + ol * (EPP / 8), vr);
       }
-    if (last_tile) {
+    if (last_tile || patch) {
       wave_lds_sync();
-      patch_last_tile<KV, DP, TT>(buf, C::VS, cur.hi - 1 - base, write_kv ? vnew : nullptr,
-                                  p.D, true, lane);
+      if (patch) patch_rows<KV, DP>(buf, C::VS, pr0, pr1, vnew, new_stride, p.D, lane);
+      if (last_tile) zero_rows<DP, TT>(buf, C::VS, cur.hi - base, lane);
     }
     wave_lds_sync();
-#pragma unroll
-    for (int r = 0; r < NG; ++r) {
-      // P^T operand: k-slot k -> token 16r + 4g + k.
-      const uint2 pw = make_uint2(pack_bf16x2(sc[4 * r + 0], sc[4 * r + 1]),
-                                  pack_bf16x2(sc[4 * r + 2], sc[4 * r + 3]));
-      const v4i16 pop = __builtin_bit_cast(v4i16, pw);
+    // V^T operands of group r + 1 are read while group r's MFMAs run.
+    auto read_va = [&](int r, v4i16* va) __attribute__((always_inline)) {
       const unsigned char* ra = buf + (16 * r + 4 * g + (n >> 2)) * C::VS + 8 * (n & 3);
-      v4i16 va[NT];
 #pragma unroll
       for (int t = 0; t < NT; ++t)
         va[t] = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
             (__attribute__((address_space(3))) v4i16*)(ra + 32 * t));
+    };
+    v4i16 va[2][NT];
+    read_va(0, va[0]);
+#pragma unroll
+    for (int r = 0; r < NG; ++r) {
+      if (r + 1 < NG) read_va(r + 1, va[(r + 1) & 1]);
+      // P^T operand: k-slot k -> token 16r + 4g + k.
+      const uint2 pw = make_uint2(pack_bf16x2(sc[4 * r + 0], sc[4 * r + 1]),
+                                  pack_bf16x2(sc[4 * r + 2], sc[4 * r + 3]));
+      const v4i16 pop = __builtin_bit_cast(v4i16, pw);
 #pragma unroll
       for (int t = 0; t < NT; ++t)
-        oacc[t] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(va[t], pop, oacc[t], 0, 0, 0);
+        oacc[t] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(va[r & 1][t], pop, oacc[t], 0, 0, 0);
     }
 
-    // ---- new token into the cache (owner of the sequence's last tile).
-    if (last_tile && write_kv)
-      write_new_token<KV, DP>(p, cache, page_indices, keys, values, cur.s, cur.h, cur.hi - 1,
-                              tq_cur, lane);
+    // ---- new tokens into the cache (owner of the tile that holds them).
+    if (patch) {
+      if constexpr (MULTI)
+        write_new_tokens<KV, DP>(p, cache, page_indices, keys, values, cur.s, cur.h, base + pr0,
+                                 base + pr1, tq_new, lane);
+      else
+        write_new_token<KV, DP>(p, cache, page_indices, keys, values, cur.s, cur.h, cur.hi - 1,
+                                tq_cur, lane);
+    }
 
     // ---- end of this wavefront's segment of a pair: the output (the whole
     // pair was this wavefront's) or a partial in slot wavefront + pair.
@@ -477,11 +558,14 @@ decode_kernel(Params p, const uint16_t* __restrict__ q, const typename KV::stora
       lsum += __shfl_xor(lsum, 16, 64);
       lsum += __shfl_xor(lsum, 32, 64);
       const int32_t s = cur.s, h = cur.h;
+      const int32_t rows = MULTI ? ql * p.qpk : min(p.qpk, 16);  // <= 16
       if (last_tile && cur.lt0 == 0) {
         if (n < rows) {
-          const float lsum_s = sum_with_sink(p, h * p.qpk + n, m_run, lsum);
+          const int32_t n_head = MULTI ? n - n_tok * p.qpk : n;
+          const float lsum_s = sum_with_sink(p, h * p.qpk + n_head, m_run, lsum);
           const float inv = lsum_s > 0.0f ? p.v_scale / lsum_s : 0.0f;
-          const int64_t orow_i = static_cast<int64_t>(tq_cur) * p.Hq + h * p.qpk + n;
+          const int64_t orow_i =
+              static_cast<int64_t>(tq_cur + (MULTI ? n_tok : 0)) * p.Hq + h * p.qpk + n_head;
           if (p.lse != nullptr && g == 0) p.lse[orow_i] = lse_from_log2(m_run, lsum);
           OutS* orow = out + orow_i * p.D;
 #pragma unroll
@@ -525,17 +609,17 @@ hipError_t launch_typed(const Params& p, const DecodeWorkspace& ws, const void* 
                         void* out, hipStream_t stream) {
   using E = typename KV::storage;
   const dim3 grid(p.decode_waves / kWaves), block(kThreads);
-  if (p.D == DP) {
-    hipLaunchKernelGGL((decode_kernel<KV, DP, OutS, true>), grid, block, 0, stream, p,
-                       static_cast<const uint16_t*>(q), static_cast<const E*>(k),
-                       static_cast<const E*>(v), static_cast<E*>(cache), kv_lens, page_indices,
-                       cu, dist, static_cast<OutS*>(out), ws.part_o, ws.part_ml, ws.plan);
-  } else {
-    hipLaunchKernelGGL((decode_kernel<KV, DP, OutS, false>), grid, block, 0, stream, p,
-                       static_cast<const uint16_t*>(q), static_cast<const E*>(k),
-                       static_cast<const E*>(v), static_cast<E*>(cache), kv_lens, page_indices,
-                       cu, dist, static_cast<OutS*>(out), ws.part_o, ws.part_ml, ws.plan);
-  }
+#define RPA_DECODE_LAUNCH(FULL, MULTI)                                                        \
+  hipLaunchKernelGGL((decode_kernel<KV, DP, OutS, FULL, MULTI>), grid, block, 0, stream, p,   \
+                     static_cast<const uint16_t*>(q), static_cast<const E*>(k),               \
+                     static_cast<const E*>(v), static_cast<E*>(cache), kv_lens, page_indices, \
+                     cu, dist, static_cast<OutS*>(out), ws.part_o, ws.part_ml, ws.plan)
+  const bool full = p.D == DP, multi = p.dq > 1;
+  if (full && !multi) RPA_DECODE_LAUNCH(true, false);
+  else if (full) RPA_DECODE_LAUNCH(true, true);
+  else if (!multi) RPA_DECODE_LAUNCH(false, false);
+  else RPA_DECODE_LAUNCH(false, true);
+#undef RPA_DECODE_LAUNCH
   return hipGetLastError();
 }
 
@@ -608,7 +692,7 @@ static int64_t decode_slots(const Params& p) {
 // Workspace layout: the partials, then the published plan.  Nothing in it
 // needs initialising.
 size_t decode_workspace_bytes(const Params& p) {
-  const int64_t rows = decode_slot_rows(p.qpk);
+  const int64_t rows = decode_slot_rows(p.qpk * p.dq);
   const int64_t slots = decode_slots(p);
   size_t bytes = 256;
   bytes += static_cast<size_t>(slots) * rows * p.Dp * sizeof(float);  // part_o
@@ -619,7 +703,7 @@ size_t decode_workspace_bytes(const Params& p) {
 
 DecodeWorkspace carve_decode_workspace(const Params& p, void* base) {
   DecodeWorkspace ws;
-  const int64_t rows = decode_slot_rows(p.qpk);
+  const int64_t rows = decode_slot_rows(p.qpk * p.dq);
   ws.slots = decode_slots(p);
   uintptr_t ptr = (reinterpret_cast<uintptr_t>(base) + 255) & ~static_cast<uintptr_t>(255);
   ws.part_o = reinterpret_cast<float*>(ptr);

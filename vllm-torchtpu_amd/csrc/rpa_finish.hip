@@ -64,7 +64,7 @@ finish_kernel(Params p, const uint16_t* __restrict__ q, const typename KVT::stor
   const int64_t nw = static_cast<int64_t>(gridDim.x) * kWaves;
   for (int64_t it = gw; it < total; it += nw) {
     if (it < nmerge) {
-      finish_merge_item<DP, OutS>(p, pv, static_cast<int32_t>(it), part_o, part_ml, out);
+      finish_merge_item<DP, OutS>(p, pv, static_cast<int32_t>(it), cu, part_o, part_ml, out);
       continue;
     }
     if (it < static_cast<int64_t>(nmerge) + nwrite) {

@@ -21,6 +21,7 @@ namespace rpa {
 // Merge item `it` (pair index) with the decode kernel's published plan.
 template <int DP, typename OutS>
 __device__ __forceinline__ void finish_merge_item(const Params& p, const PlanView& pv, int32_t it,
+                                                  const int32_t* __restrict__ cu,
                                                   const float* __restrict__ part_o,
                                                   const float* __restrict__ part_ml,
                                                   OutS* __restrict__ out) {
@@ -36,14 +37,16 @@ __device__ __forceinline__ void finish_merge_item(const Params& p, const PlanVie
   if (wa == wb) return;  // one wavefront finished the pair
   const int32_t first = wa + it;
   const int32_t nparts = wb - wa + 1;
-  const int32_t rows = min(p.qpk, 16);
-  const int64_t orow0 = static_cast<int64_t>(pv.tq[s]) * p.Hq + h * p.qpk;
-  switch (decode_slot_rows(p.qpk)) {
-    case 1: merge_partials<DP, 1>(p, part_o, part_ml, first, nparts, rows, out, orow0); break;
-    case 2: merge_partials<DP, 2>(p, part_o, part_ml, first, nparts, rows, out, orow0); break;
-    case 4: merge_partials<DP, 4>(p, part_o, part_ml, first, nparts, rows, out, orow0); break;
-    case 8: merge_partials<DP, 8>(p, part_o, part_ml, first, nparts, rows, out, orow0); break;
-    default: merge_partials<DP, 16>(p, part_o, part_ml, first, nparts, rows, out, orow0); break;
+  // The decode group's rows: q_len tokens x qpk heads (q_len * qpk <= 16).
+  const int32_t ql = p.dq > 1 ? min(max(cu[s + 1] - cu[s], 1), p.dq) : 1;
+  const int32_t rows = min(ql * p.qpk, 16);
+  const int32_t tq = pv.tq[s];
+  switch (decode_slot_rows(p.qpk * p.dq)) {
+    case 1: merge_partials<DP, 1>(p, part_o, part_ml, first, nparts, rows, out, tq, h); break;
+    case 2: merge_partials<DP, 2>(p, part_o, part_ml, first, nparts, rows, out, tq, h); break;
+    case 4: merge_partials<DP, 4>(p, part_o, part_ml, first, nparts, rows, out, tq, h); break;
+    case 8: merge_partials<DP, 8>(p, part_o, part_ml, first, nparts, rows, out, tq, h); break;
+    default: merge_partials<DP, 16>(p, part_o, part_ml, first, nparts, rows, out, tq, h); break;
   }
 }
 

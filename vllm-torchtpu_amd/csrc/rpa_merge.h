@@ -13,7 +13,7 @@
 namespace rpa {
 
 // Merge the `nunits` partials of one (sequence, kv head) and write its output
-// rows [0, rows).  Partial k sits in slot first + k: RP rows
+// rows [0, rows): row r is token tq + r / qpk, q head h * qpk + r % qpk.  Partial k sits in slot first + k: RP rows
 // x DP floats of un-normalised O, and RP (m, l) pairs (log2 units).  One
 // wavefront; lane e of load j covers element e + 64 j of a slot, so every
 // load is a wave-wide contiguous 256-byte read and row (j * 64 / DP) is the
@@ -32,7 +32,7 @@ template <int DP, int RP, typename OutS>
 __device__ __forceinline__ void merge_partials(const Params& p, const float* __restrict__ part_o,
                                                const float* __restrict__ part_ml, int32_t first,
                                                int32_t nunits, int32_t rows,
-                                               OutS* __restrict__ out, int64_t orow0) {
+                                               OutS* __restrict__ out, int32_t tq, int32_t h) {
   constexpr int NDW = RP * DP / 64;  // dwords per lane per slot
   constexpr int UB = NDW >= 64 ? 1 : (64 / NDW > 16 ? 16 : 64 / NDW);  // units per batch
   const int lane = threadIdx.x & 63;
@@ -79,17 +79,33 @@ __device__ __forceinline__ void merge_partials(const Params& p, const float* __r
       ml_combine(M[r], L[r], mo, lo);
     }
   }
+  // Output row and q head of row r (one-token groups: rows r < qpk).
+  // Token of row r within the group (wavefront-uniform; 0 for one-token
+  // groups, where the division is skipped).
+  int32_t tokr[RP];
+#pragma unroll
+  for (int r = 0; r < RP; ++r) tokr[r] = 0;
+  if (p.dq > 1) {
+#pragma unroll
+    for (int r = 0; r < RP; ++r) tokr[r] = r / p.qpk;
+  }
+  const int64_t row0 = static_cast<int64_t>(tq) * p.Hq + h * p.qpk;
+  auto qhead = [&](int r) __attribute__((always_inline)) -> int32_t {
+    return h * p.qpk + r - tokr[r] * p.qpk;
+  };
+  auto orow = [&](int r) __attribute__((always_inline)) -> int64_t {
+    return row0 + r + static_cast<int64_t>(tokr[r]) * (p.Hq - p.qpk);
+  };
   float scale[RP];
-  const int32_t qh0 = static_cast<int32_t>(orow0 % p.Hq);  // q head of row 0
 #pragma unroll
   for (int r = 0; r < RP; ++r) {
-    const float ls = r < rows ? sum_with_sink(p, qh0 + r, M[r], L[r]) : L[r];
+    const float ls = r < rows ? sum_with_sink(p, qhead(r), M[r], L[r]) : L[r];
     scale[r] = ls > 0.0f ? p.v_scale / ls : 0.0f;
   }
   if (p.lse != nullptr) {
 #pragma unroll
     for (int r = 0; r < RP; ++r)
-      if (lane == r && r < rows) p.lse[orow0 + r] = lse_from_log2(M[r], L[r]);
+      if (lane == r && r < rows) p.lse[orow(r)] = lse_from_log2(M[r], L[r]);
   }
 
   float acc[NDW];
@@ -136,7 +152,7 @@ __device__ __forceinline__ void merge_partials(const Params& p, const float* __r
   for (int j = 0; j < NDW; ++j) {
     const int r = j * 64 / DP;
     const int d = lane + 64 * (j % (DP / 64));
-    if (r < rows && d < p.D) store_out(out, (orow0 + r) * p.D + d, acc[j]);
+    if (r < rows && d < p.D) store_out(out, orow(r) * p.D + d, acc[j]);
   }
 }
 

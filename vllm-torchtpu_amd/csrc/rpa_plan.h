@@ -52,6 +52,7 @@ struct PlanCoreT {
   int32_t base[N + 1];   // exclusive prefix of tiles per sequence; base[n] = total
   int32_t dkv[N];        // kv_len of a decode sequence (clamped), else 0
   int32_t tq[N];         // q row of the sequence (cu_q_lens[s], clamped)
+  int32_t ql[N];         // q_len of a decode sequence, else 0
   int32_t red[3 * kPlanWaves];
 };
 using PlanCore = PlanCoreT<kMaxDecodeSeqs>;
@@ -60,20 +61,26 @@ struct PlanRows {
   int32_t cu[kMaxDecodeSeqs + 1];     // cu_q_lens[0 .. num_seqs]
 };
 
-__device__ __forceinline__ void decode_range(const Params& p, int32_t kv_len, int32_t* lo,
-                                             int32_t* hi) {
+// Keys [lo, hi) that some row of a decode group of q_len tokens attends:
+// under a causal window the first token (position kv_len - q_len) sees back
+// to kv_len - q_len - W + 1.
+__device__ __forceinline__ void decode_range(const Params& p, int32_t kv_len, int32_t q_len,
+                                             int32_t* lo, int32_t* hi) {
   *hi = kv_len;
-  *lo = (p.causal && p.window > 0) ? max(0, kv_len - p.window) : 0;
+  *lo = (p.causal && p.window > 0) ? max(0, kv_len - q_len - p.window + 1) : 0;
 }
 
+// A decode sequence has 1 <= q_len <= dq new tokens (their q_len * qpk rows
+// fit the decode kernel's 16 MFMA columns), inside the token and key ranges.
 __device__ __forceinline__ bool is_decode_seq(const Params& p, const int32_t* cu,
                                               const int32_t* kv_lens, int32_t s,
-                                              int32_t* kv_len_out) {
+                                              int32_t* kv_len_out, int32_t* q_len_out) {
   const int32_t q_len = cu[s + 1] - cu[s];
   int32_t kv_len = kv_lens[s];
   kv_len = min(kv_len, p.pps * p.ps);
   *kv_len_out = kv_len;
-  return q_len == 1 && kv_len >= 1 && cu[s] >= 0 && cu[s] < p.T;
+  *q_len_out = q_len;
+  return q_len >= 1 && q_len <= p.dq && kv_len >= q_len && cu[s] >= 0 && cu[s] + q_len <= p.T;
 }
 
 // In-place exclusive scan of a[0..n) (values >= 0); a[n] = total.
@@ -101,11 +108,13 @@ __device__ __forceinline__ void block_exclusive_scan(int32_t* a, int32_t n, int3
   __syncthreads();
 }
 
-// Tiles of a decode sequence with kv_len dkv (0 for a non-decode sequence).
-__device__ __forceinline__ int32_t decode_tiles(const Params& p, int32_t dkv, int32_t tile) {
+// Tiles of a decode sequence with kv_len dkv and q_len ql (0 for a
+// non-decode sequence).
+__device__ __forceinline__ int32_t decode_tiles(const Params& p, int32_t dkv, int32_t ql,
+                                                int32_t tile) {
   if (dkv <= 0) return 0;
   int32_t lo, hi;
-  decode_range(p, dkv, &lo, &hi);
+  decode_range(p, dkv, ql, &lo, &hi);
   return (hi - lo + tile - 1) / tile;
 }
 
@@ -127,12 +136,13 @@ __device__ __forceinline__ Plan build_plan(const Params& p, const int32_t* kv_le
   // first kPlanThreads threads only: the reduction slots hold kPlanWaves waves.
   const bool planner = tid < kPlanThreads;
   for (int32_t s = planner ? tid : n; s < n; s += kPlanThreads) {
-    int32_t kl;
-    const bool dec = is_decode_seq(p, cu, kv_lens, s, &kl) && decode_enabled;
-    const int32_t nt = dec ? decode_tiles(p, kl, tile) : 0;
+    int32_t kl, ql;
+    const bool dec = is_decode_seq(p, cu, kv_lens, s, &kl, &ql) && decode_enabled;
+    const int32_t nt = dec ? decode_tiles(p, kl, ql, tile) : 0;
     seqs += dec ? 1 : 0;
     others += (!dec && cu[s + 1] > cu[s]) ? 1 : 0;
     L.dkv[s] = dec ? kl : 0;
+    L.ql[s] = dec ? ql : 0;
     L.tq[s] = min(max(cu[s], 0), max(p.T - 1, 0));
     L.base[s] = nt;  // scanned into the prefix below
     if (R != nullptr) {
@@ -220,10 +230,11 @@ __device__ __forceinline__ int32_t find_prefix(const int32_t* prefix, int32_t n,
   return lo;
 }
 
-// Rows of a partial slot: min(q_heads_per_kv_head, 16) rounded up to a power
-// of two (padding rows are never written and never output).
-__host__ __device__ constexpr int decode_slot_rows(int qpk) {
-  int r = qpk < 16 ? qpk : 16;
+// Rows of a partial slot: the largest decode row group, min(dq * qpk, 16),
+// rounded up to a power of two (padding rows are never written and never
+// output).
+__host__ __device__ constexpr int decode_slot_rows(int group_rows) {
+  int r = group_rows < 16 ? group_rows : 16;
   int rp = 1;
   while (rp < r) rp *= 2;
   return rp;

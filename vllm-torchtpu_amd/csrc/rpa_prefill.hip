@@ -113,8 +113,11 @@ struct PrefillCfg {
   static constexpr int NT = DP / 32;               // 32-dim output blocks
   static_assert(THREADS % PPK == 0 && BK % KPI == 0, "whole pieces per thread");
   static_assert(THREADS >= kPlanThreads && 3 * kPlanWaves >= THREADS / 64, "plan scan fits");
-  static_assert(2 * BUF >= 4 * (kMaxDecodeSeqs + 1), "plan scratch fits the tile buffers");
-  static_assert(2 * BUF >= sizeof(PlanCore) + sizeof(PlanRows), "finish plan fits the tile buffers");
+  // LDS of the tile buffers, which also hold the block prefix of the
+  // attention role and the plan of the finish role (at least that much).
+  static constexpr int PLAN_BYTES = static_cast<int>(sizeof(PlanCore) + sizeof(PlanRows));
+  static constexpr int SMEM = 2 * BUF > PLAN_BYTES ? 2 * BUF : PLAN_BYTES;
+  static_assert(SMEM >= 4 * (kMaxDecodeSeqs + 1), "plan scratch fits the tile buffers");
 };
 
 // Page ids of an item's key range kept in LDS (longer ranges read the page
@@ -129,8 +132,8 @@ constexpr float kRescaleLog2 = 8.0f;
 __device__ __forceinline__ int32_t prefill_blocks(const Params& p, const int32_t* cu,
                                                   const int32_t* kv_lens, int32_t s, int32_t bq,
                                                   bool decode_on) {
-  int32_t kl;
-  if (decode_on && is_decode_seq(p, cu, kv_lens, s, &kl)) return 0;
+  int32_t kl, ql;
+  if (decode_on && is_decode_seq(p, cu, kv_lens, s, &kl, &ql)) return 0;
   const int32_t q_len = cu[s + 1] - cu[s];
   if (q_len <= 0) return 0;
   return (q_len + bq - 1) / bq;
@@ -164,7 +167,7 @@ __device__ __forceinline__ void prefill_finish_role(
   const int32_t nw = nfin * pw;
   for (int32_t it = fb * pw + wave; it < total; it += nw) {
     if (merges)
-      finish_merge_item<DP, OutS>(p, pv, it, part_o, part_ml, out);
+      finish_merge_item<DP, OutS>(p, pv, it, cu, part_o, part_ml, out);
     else
       finish_write_item<E>(p, decode_on, pv, pl_rows, n, cu, kv_lens, cache, page_indices, keys,
                            values, it, lane);
@@ -187,7 +190,7 @@ prefill_kernel(Params p, const uint16_t* __restrict__ q,
   using C = PrefillCfg<DP>;
   using E = typename KV::storage;
   constexpr int BK = C::BK;
-  __shared__ __align__(16) unsigned char smem[2 * C::BUF];
+  __shared__ __align__(16) unsigned char smem[C::SMEM];
   __shared__ int32_t pages[kItemPages];
   __shared__ int32_t red[3 * kPlanWaves];
   // Key address table, three tiles: [t % 3][key] = {K row, V row}.

@@ -228,7 +228,7 @@ def dynamic_validate_inputs(queries, keys, values, kv_cache, kv_lens, page_indic
 # ---------------------------------------------------------------------------
 def _make_desc(q, k, kv_cache, kv_lens, page_indices, out_dtype, *, use_causal_mask,
                skip_kv_update, sm_scale, sliding_window, soft_cap, q_scale, k_scale,
-               v_scale, path=N.RPA_PATH_AUTO) -> N.RpaDesc:
+               v_scale, path=N.RPA_PATH_AUTO, decode_query_size=1) -> N.RpaDesc:
     d = N.RpaDesc()
     d.abi_version = N.ABI_VERSION
     d.q_dtype = N.rpa_dtype(q.dtype)
@@ -255,6 +255,7 @@ def _make_desc(q, k, kv_cache, kv_lens, page_indices, out_dtype, *, use_causal_m
     d.k_scale = 1.0 if k_scale is None else float(k_scale)
     d.v_scale = 1.0 if v_scale is None else float(v_scale)
     d.path = int(path)
+    d.decode_query_size = int(decode_query_size)
     return d
 
 
@@ -292,7 +293,8 @@ def _workspace(device: torch.device, nbytes: int) -> torch.Tensor:
 def _rpa_forward_impl(queries, keys, values, kv_cache, kv_lens, page_indices, cu_q_lens,
                       distribution, out, *, use_causal_mask, skip_kv_update, sm_scale,
                       sliding_window, soft_cap, q_scale, k_scale, v_scale,
-                      path=N.RPA_PATH_AUTO, workspace=None, lse=None, attention_sink=None):
+                      path=N.RPA_PATH_AUTO, workspace=None, lse=None, attention_sink=None,
+                      decode_query_size=1):
     L = N.lib()
     _require_device(queries, keys, values, kv_cache, kv_lens, page_indices, cu_q_lens,
                     distribution, out)
@@ -305,7 +307,8 @@ def _rpa_forward_impl(queries, keys, values, kv_cache, kv_lens, page_indices, cu
     desc = _make_desc(queries, keys, kv_cache, kv_lens, page_indices, out.dtype,
                       use_causal_mask=use_causal_mask, skip_kv_update=skip_kv_update,
                       sm_scale=sm_scale, sliding_window=sliding_window, soft_cap=soft_cap,
-                      q_scale=q_scale, k_scale=k_scale, v_scale=v_scale, path=path)
+                      q_scale=q_scale, k_scale=k_scale, v_scale=v_scale, path=path,
+                      decode_query_size=decode_query_size)
     N.check(L.rpa_validate_desc(desc), "rpa_validate_desc")
     with torch.cuda.device(queries.device):
         ws_bytes = int(L.rpa_workspace_size(desc))
@@ -341,20 +344,21 @@ def _rpa_op(queries: torch.Tensor, keys: torch.Tensor, values: torch.Tensor,
             cu_q_lens: torch.Tensor, distribution: torch.Tensor, out_dtype: torch.dtype,
             use_causal_mask: bool, skip_kv_update: bool, sm_scale: float,
             sliding_window: int, soft_cap: float, has_soft_cap: bool, q_scale: float,
-            k_scale: float, v_scale: float, path: int) -> torch.Tensor:
+            k_scale: float, v_scale: float, path: int,
+            decode_query_size: int) -> torch.Tensor:
     out = torch.empty(queries.shape, dtype=out_dtype, device=queries.device)
     return _rpa_forward_impl(
         queries, keys, values, kv_cache, kv_lens, page_indices, cu_q_lens, distribution, out,
         use_causal_mask=use_causal_mask, skip_kv_update=skip_kv_update, sm_scale=sm_scale,
         sliding_window=sliding_window if sliding_window > 0 else None,
         soft_cap=soft_cap if has_soft_cap else None, q_scale=q_scale, k_scale=k_scale,
-        v_scale=v_scale, path=path)
+        v_scale=v_scale, path=path, decode_query_size=decode_query_size)
 
 
 @_rpa_op.register_fake
 def _(queries, keys, values, kv_cache, kv_lens, page_indices, cu_q_lens, distribution,
       out_dtype, use_causal_mask, skip_kv_update, sm_scale, sliding_window, soft_cap,
-      has_soft_cap, q_scale, k_scale, v_scale, path):
+      has_soft_cap, q_scale, k_scale, v_scale, path, decode_query_size):
     return torch.empty(queries.shape, dtype=out_dtype, device=queries.device)
 
 
@@ -366,8 +370,8 @@ def _rpa_lse_op(queries: torch.Tensor, keys: torch.Tensor, values: torch.Tensor,
                 cu_q_lens: torch.Tensor, distribution: torch.Tensor, out_dtype: torch.dtype,
                 use_causal_mask: bool, skip_kv_update: bool, sm_scale: float,
                 sliding_window: int, soft_cap: float, has_soft_cap: bool, q_scale: float,
-                k_scale: float, v_scale: float,
-                path: int) -> tuple[torch.Tensor, torch.Tensor]:
+                k_scale: float, v_scale: float, path: int,
+                decode_query_size: int) -> tuple[torch.Tensor, torch.Tensor]:
     out = torch.empty(queries.shape, dtype=out_dtype, device=queries.device)
     lse = torch.full(queries.shape[:2], float("-inf"), dtype=torch.float32,
                      device=queries.device)
@@ -376,14 +380,14 @@ def _rpa_lse_op(queries: torch.Tensor, keys: torch.Tensor, values: torch.Tensor,
         use_causal_mask=use_causal_mask, skip_kv_update=skip_kv_update, sm_scale=sm_scale,
         sliding_window=sliding_window if sliding_window > 0 else None,
         soft_cap=soft_cap if has_soft_cap else None, q_scale=q_scale, k_scale=k_scale,
-        v_scale=v_scale, path=path, lse=lse)
+        v_scale=v_scale, path=path, lse=lse, decode_query_size=decode_query_size)
     return out, lse
 
 
 @_rpa_lse_op.register_fake
 def _(queries, keys, values, kv_cache, kv_lens, page_indices, cu_q_lens, distribution,
       out_dtype, use_causal_mask, skip_kv_update, sm_scale, sliding_window, soft_cap,
-      has_soft_cap, q_scale, k_scale, v_scale, path):
+      has_soft_cap, q_scale, k_scale, v_scale, path, decode_query_size):
     return (torch.empty(queries.shape, dtype=out_dtype, device=queries.device),
             torch.empty(queries.shape[:2], dtype=torch.float32, device=queries.device))
 
@@ -419,6 +423,7 @@ def ragged_paged_attention(
     disable_bounds_checks: bool = True,
     disable_semaphore_checks: bool = True,
     return_lse: bool = False,
+    decode_query_size: int = 1,
 ):
     """Ragged paged attention with mixed prefill and decode (kernel.py:1633-1984).
 
@@ -432,6 +437,12 @@ def ragged_paged_attention(
     natural-log log-sum-exp m + log(l) of each computed row's logits (after
     scaling and soft cap; -inf for a row without keys, and for rows past
     cu_q_lens[distribution[2]]) -- what merge_attn_results combines.
+
+    decode_query_size (the batched wrapper's, batched_rpa/wrapper.py:549,
+    :601-602): the largest number of query tokens of a decode sequence
+    (speculative-decoding verify windows of K + 1 tokens).  Sequences with up to
+    that many new tokens run on the decode kernel (while q_len * Hq/Hkv <= 16);
+    the result does not depend on it.
     """
     del debug_mode, disable_bounds_checks, disable_semaphore_checks
     static_validate_inputs(
@@ -442,6 +453,8 @@ def ragged_paged_attention(
         chunk_prefill_size=chunk_prefill_size, d_block_sizes=d_block_sizes,
         p_block_sizes=p_block_sizes, m_block_sizes=m_block_sizes,
         vmem_limit_bytes=vmem_limit_bytes)
+    if int(decode_query_size) < 1:
+        raise ValueError(f"{decode_query_size=} must be positive.")
     if mask_value is not None and mask_value > -1e30:
         # Masked logits are excluded with weight exactly 0; that equals the
         # reference only when exp(mask_value - rowmax) underflows.
@@ -462,7 +475,7 @@ def ragged_paged_attention(
         float(sm_scale), 0 if sliding_window is None else int(sliding_window),
         0.0 if soft_cap is None else float(soft_cap), soft_cap is not None,
         1.0 if q_scale is None else float(q_scale), 1.0 if k_scale is None else float(k_scale),
-        1.0 if v_scale is None else float(v_scale), N.RPA_PATH_AUTO)
+        1.0 if v_scale is None else float(v_scale), N.RPA_PATH_AUTO, int(decode_query_size))
     if return_lse:
         out, lse = res
         return out, kv_cache, lse
