@@ -247,6 +247,13 @@ int rpa_forward_ex(const rpa_desc* d, const void* queries, const void* keys, con
     hipError_t e = rpa::launch_prefill(p, d->kv_dtype, d->out_dtype, queries, keys, values,
                                        kv_cache, kv_lens, page_indices, cu_q_lens, distribution,
                                        out, ws, cus, s);
+    if (e != hipSuccess) return RPA_ERR_LAUNCH;
+    if (rpa::prefill_has_finish_roles(p) || (p.decode_waves <= 0 && d->skip_kv_update))
+      return RPA_OK;
+    // Merges and cache writes in a finish launch after the prefill kernel
+    // (which reads new tokens from k/v, never from the pages being written).
+    e = rpa::launch_finish(p, d->kv_dtype, d->out_dtype, ws, queries, keys, values, kv_cache,
+                           kv_lens, page_indices, cu_q_lens, distribution, out, cus, s);
     return e == hipSuccess ? RPA_OK : RPA_ERR_LAUNCH;
   }
   hipError_t e = rpa::launch_finish(p, d->kv_dtype, d->out_dtype, ws, queries, keys, values,

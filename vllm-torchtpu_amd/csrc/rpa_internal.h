@@ -69,7 +69,11 @@ hipError_t launch_decode(const Params& p, int kv_dtype, int out_dtype, const Dec
 // Prefill kernel: MFMA attention of every row the decode kernel does not
 // take (new tokens read from k/v), plus, in finish workgroups appended to its
 // grid, the finish kernel's merge and write items (the finish kernel is then
-// not launched).
+// not launched) -- at padded head_dim <= 128.  At 256 the finish kernel runs
+// after it with the merge and write items.
+template <int DP>
+constexpr bool kPrefillFinishRoles = DP <= 128;
+inline bool prefill_has_finish_roles(const Params& p) { return p.Dp <= 128; }
 bool prefill_supported(const Params& p, int q_dtype, int kv_dtype, int out_dtype);
 int prefill_merge_blocks(const Params& p, int num_cus);
 int prefill_write_blocks(const Params& p, int num_cus);

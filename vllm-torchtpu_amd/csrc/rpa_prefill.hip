@@ -206,13 +206,17 @@ prefill_kernel(Params p, const uint16_t* __restrict__ q,
   // ---- finish workgroups: [0, nfm) merge items, the last nfw write items.
   const int32_t blk_id = static_cast<int32_t>(blockIdx.x);
   const int32_t nattn = static_cast<int32_t>(gridDim.x) - nfm - nfw;
-  if (blk_id < nfm || blk_id >= nfm + nattn) {
-    const bool merges = blk_id < nfm;
-    prefill_finish_role<E, DP, OutS>(p, smem, keys, values, cache, kv_lens, page_indices, cu,
-                                     dist, out, plan, part_o, part_ml, merges,
-                                     merges ? nfm : nfw, merges ? blk_id : blk_id - nfm - nattn,
-                                     C::THREADS / 64);
-    return;
+  // At head_dim 256 the finish work runs in the finish kernel instead: inlined
+  // here it costs the attention loop of that instance about 10% (measured).
+  if constexpr (kPrefillFinishRoles<DP>) {
+    if (blk_id < nfm || blk_id >= nfm + nattn) {
+      const bool merges = blk_id < nfm;
+      prefill_finish_role<E, DP, OutS>(p, smem, keys, values, cache, kv_lens, page_indices, cu,
+                                       dist, out, plan, part_o, part_ml, merges,
+                                       merges ? nfm : nfw, merges ? blk_id : blk_id - nfm - nattn,
+                                       C::THREADS / 64);
+      return;
+    }
   }
   // Attention block index (nfm is a multiple of 8, so bid % 8 and blockIdx.x
   // % 8 -- the XCD the dispatcher picks -- agree).
@@ -633,7 +637,7 @@ bool prefill_supported(const Params& p, int q_dtype, int kv_dtype, int out_dtype
 // every possible pair, at most two per CU (the kernel's occupancy), a
 // multiple of 8 so the attention blocks keep their XCD placement.
 int prefill_merge_blocks(const Params& p, int num_cus) {
-  if (p.decode_waves <= 0) return 0;
+  if (p.decode_waves <= 0 || !prefill_has_finish_roles(p)) return 0;
   int64_t b = (static_cast<int64_t>(p.S) * p.Hkv + 3) / 4;
   b = b > 2 * num_cus ? 2 * num_cus : b;
   return static_cast<int>((b + 7) / 8 * 8);
@@ -642,7 +646,7 @@ int prefill_merge_blocks(const Params& p, int num_cus) {
 // Write workgroups (end of the grid): about 16 token rows each, at most one
 // per CU.
 int prefill_write_blocks(const Params& p, int num_cus) {
-  if (p.skip_kv_update || p.T == 0) return 0;
+  if (p.skip_kv_update || p.T == 0 || !prefill_has_finish_roles(p)) return 0;
   int64_t b = (static_cast<int64_t>(p.T) + 15) / 16;
   return static_cast<int>(b > num_cus ? num_cus : b);
 }
