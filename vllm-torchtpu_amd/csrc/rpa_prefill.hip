@@ -379,43 +379,68 @@ prefill_kernel(Params p, const uint16_t* __restrict__ q,
     if (!(wave_live && k0 < w_hi1 && k0 + BK > w_lo0)) return;
     {
       // S^T = K . Q^T per 32-key sub-block (A lane l -> key l % 32, dims
-      // 16kk + 8 half ..), sub-block-major: sub-block 0's scores are final
-      // while sub-block 1's MFMAs still run, so its softmax (VALU) overlaps
-      // them; likewise sub-block 1's softmax overlaps sub-block 0's PV MFMAs.
-      f32x16_t sacc[C::NSB];
-#pragma unroll
-      for (int sb = 0; sb < C::NSB; ++sb) {
-        sacc[sb] = f32x16_t{};
+      // 16kk + 8 half ..).  With several sub-blocks (head_dim <= 128, two
+      // wavefronts per SIMD) each sub-block runs S^T, its softmax, then
+      // O^T += V^T . P^T: one 16-VGPR score accumulator is live, which leaves
+      // room for the K operand reads to run kRA k-steps ahead of their MFMAs.
+      // With one sub-block (head_dim 256) S^T comes first, as a whole.
+      constexpr int kRA = 4;  // K operand reads in flight
+      f32x16_t sacc1 = f32x16_t{};
+      if constexpr (C::NSB == 1) {
 #pragma unroll
         for (int kk = 0; kk < C::KSTEPS; ++kk) {
           const uint4 kv = *reinterpret_cast<const uint4*>(
-              kbuf + (32 * sb + col) * C::KS + 2 * (16 * kk + 8 * half));
-          sacc[sb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
-              __builtin_bit_cast(bf16x8_t, kv), __builtin_bit_cast(bf16x8_t, qop[kk]), sacc[sb],
+              kbuf + col * C::KS + 2 * (16 * kk + 8 * half));
+          sacc1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+              __builtin_bit_cast(bf16x8_t, kv), __builtin_bit_cast(bf16x8_t, qop[kk]), sacc1,
               0, 0, 0);
         }
-      }
-      // Schedule: the K operand reads run four MFMAs ahead of their use (LDS
-      // latency is several MFMA durations).
-      constexpr int kS = C::NSB * C::KSTEPS;  // S^T MFMAs (and K reads) per tile
-      __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, kRA, 0);
 #pragma unroll
-      for (int i = 0; i < kS - 4; ++i) {
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        for (int i = 0; i < C::KSTEPS - kRA; ++i) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+          __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        }
+        __builtin_amdgcn_sched_group_barrier(0x008, kRA, 0);
       }
-      __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
       // Masks only where some row of the wavefront does not see the whole tile.
       const bool need_mask = !(k0 >= w_lo1 && k0 + BK <= w_hi0);
       const int G = lane >> 4, jl = lane & 15;
 #pragma unroll
       for (int sb = 0; sb < C::NSB; ++sb) {
+        f32x16_t sacc = sacc1;
+        if constexpr (C::NSB > 1) {
+          // Explicit ring of kRA operands (two wavefronts per SIMD: registers
+          // are short, and without it the reads end up one MFMA ahead).
+          auto kread = [&](int kk) __attribute__((always_inline)) -> uint4 {
+            return *reinterpret_cast<const uint4*>(kbuf + (32 * sb + col) * C::KS +
+                                                   2 * (16 * kk + 8 * half));
+          };
+          uint4 kb[kRA];
+#pragma unroll
+          for (int i = 0; i < kRA; ++i) kb[i] = kread(i);
+#pragma unroll
+          for (int kk = 0; kk < C::KSTEPS; ++kk) {
+            const uint4 kv = kb[kk % kRA];
+            if (kk + kRA < C::KSTEPS) kb[kk % kRA] = kread(kk + kRA);
+            sacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+                __builtin_bit_cast(bf16x8_t, kv), __builtin_bit_cast(bf16x8_t, qop[kk]), sacc,
+                0, 0, 0);
+          }
+          __builtin_amdgcn_sched_group_barrier(0x100, kRA, 0);
+#pragma unroll
+          for (int i = 0; i < C::KSTEPS - kRA; ++i) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+          }
+          __builtin_amdgcn_sched_group_barrier(0x008, kRA, 0);
+        }
         // Scores y (raw logits, or soft-capped logits in log2 units); register
         // i -> key k0 + 32 sb + 8(i/4) + 4 half + i%4.
         float y[16];
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
-          float x = sacc[sb][i];
+          float x = sacc[i];
           if (p.has_cap) x = soft_cap_fn(x * p.score_scale, p.cap, p.inv_cap) * kLog2e;
           y[i] = x;
         }
