@@ -495,26 +495,43 @@ prefill_kernel(Params p, const uint16_t* __restrict__ q,
         // 32 sb + 16 ks + 4 half + 0..3, slots 4..7 -> the same + 8.
         // ds_read_b64_tr_b16 in 16-lane group G: source lane j points at key
         // kbase + j / 4, dims d0 + 4 (j % 4); lane n receives V[kbase + 0..3][d0 + n].
-#pragma unroll
-        for (int ks = 0; ks < 2; ++ks) {
+        constexpr int kP = 2 * C::NT;  // PV MFMAs per sub-block: (ks, tt)
+        auto vread = [&](int i) __attribute__((always_inline)) -> uint4 {
+          const int ks = i / C::NT, tt = i % C::NT;
           const int key_a = 32 * sb + 16 * ks + 4 * (G >> 1) + (jl >> 2);
-          const unsigned char* ra = vbuf + key_a * C::VS + 2 * (16 * (G & 1) + 4 * (jl & 3));
-          const unsigned char* rb = ra + 8 * C::VS;
+          const unsigned char* ra =
+              vbuf + key_a * C::VS + 2 * (16 * (G & 1) + 4 * (jl & 3)) + 64 * tt;
+          const v4i16 va = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+              (__attribute__((address_space(3))) v4i16*)ra);
+          const v4i16 vb = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+              (__attribute__((address_space(3))) v4i16*)(ra + 8 * C::VS));
+          const uint2 ua = __builtin_bit_cast(uint2, va), ub = __builtin_bit_cast(uint2, vb);
+          return make_uint4(ua.x, ua.y, ub.x, ub.y);
+        };
+        if constexpr (C::NSB > 1) {
+          // The V^T operands of MFMA i + 2 are read before MFMA i issues.
+          uint4 vb2[2];
+          vb2[0] = vread(0);
+          vb2[1] = vread(1);
 #pragma unroll
-          for (int tt = 0; tt < C::NT; ++tt) {
-            const v4i16 va = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                (__attribute__((address_space(3))) v4i16*)(ra + 64 * tt));
-            const v4i16 vb = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                (__attribute__((address_space(3))) v4i16*)(rb + 64 * tt));
-            const uint2 ua = __builtin_bit_cast(uint2, va), ub = __builtin_bit_cast(uint2, vb);
-            const uint4 vop = make_uint4(ua.x, ua.y, ub.x, ub.y);
+          for (int i = 0; i < kP; ++i) {
+            const uint4 vop = vb2[i & 1];
+            if (i + 2 < kP) vb2[i & 1] = vread(i + 2);
+            const int tt = i % C::NT;
             oacc[tt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
-                __builtin_bit_cast(bf16x8_t, vop), __builtin_bit_cast(bf16x8_t, pops[ks]),
+                __builtin_bit_cast(bf16x8_t, vop), __builtin_bit_cast(bf16x8_t, pops[i / C::NT]),
                 oacc[tt], 0, 0, 0);
+          }
+        } else {
+#pragma unroll
+          for (int i = 0; i < kP; ++i) {
+            const int tt = i % C::NT;
+            oacc[tt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+                __builtin_bit_cast(bf16x8_t, vread(i)),
+                __builtin_bit_cast(bf16x8_t, pops[i / C::NT]), oacc[tt], 0, 0, 0);
           }
         }
         // Schedule: the V^T reads (two per MFMA) run two MFMAs ahead.
-        constexpr int kP = 2 * C::NT;  // PV MFMAs per sub-block
         __builtin_amdgcn_sched_group_barrier(0x100, 4, 1);
 #pragma unroll
         for (int i = 0; i < kP - 2; ++i) {
