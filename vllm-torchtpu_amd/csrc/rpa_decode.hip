@@ -268,11 +268,13 @@ decode_kernel(Params p, const uint16_t* __restrict__ q, const typename KV::stora
   const int ol = lane & 7;   // load shape: 16-byte column within a 128-byte part
 
   const Plan pl = build_plan(p, kv_lens, cu, dist, TT, true, L, nullptr);
-  publish_plan(p, pl, L, cu, plan_ws);
   const int32_t gw = static_cast<int32_t>(blockIdx.x) * kWaves + wave;
   // This wavefront's stretch [g_begin, g_end) of the work line.
   const int64_t g_begin64 = static_cast<int64_t>(gw) * pl.tpw;
-  if (g_begin64 >= pl.total_tiles) return;  // no barrier follows the plan
+  if (g_begin64 >= pl.total_tiles) {  // no barrier follows the plan
+    publish_plan(p, pl, L, plan_ws);
+    return;
+  }
   const int32_t g_begin = static_cast<int32_t>(g_begin64);
   const int32_t g_end = min(g_begin + pl.tpw, pl.total_tiles);
   unsigned char* buf = smem + wave * C::WAVE_LDS;
@@ -373,6 +375,8 @@ decode_kernel(Params p, const uint16_t* __restrict__ q, const typename KV::stora
   uint4 bufr[2][NOCT][NPART];
   Pages pbuf[2];
   pages_of(cur, pbuf[0]);
+  // The plan's stores go out while the first page ids are in flight.
+  publish_plan(p, pl, L, plan_ws);
   load_tile(cur, pbuf[0], bufr[0]);
   load_q(cur, qbuf[0]);
   TileInfo nxt = advance(cur);

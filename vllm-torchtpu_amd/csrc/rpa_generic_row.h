@@ -137,6 +137,7 @@ __device__ __forceinline__ void write_record(const Params& p, E* __restrict__ ca
                                              const E* __restrict__ values, int32_t s, int32_t j,
                                              int32_t t, int lane) {
   constexpr int EPP = 8 / sizeof(E);
+  if (j < 0 || j >= p.pps * p.ps) return;  // outside the sequence's page table
   const int32_t pg = page_indices[static_cast<int64_t>(s) * p.pps + page_of(p, j)];
   if (pg < 0 || pg >= p.P) return;
   E* rec = cache + (static_cast<int64_t>(pg) * p.ps + slot_of(p, j)) * p.rec;

@@ -53,6 +53,7 @@ struct PlanCoreT {
   int32_t dkv[N];        // kv_len of a decode sequence (clamped), else 0
   int32_t tq[N];         // q row of the sequence (cu_q_lens[s], clamped)
   int32_t ql[N];         // q_len of a decode sequence, else 0
+  int32_t cu[N + 1];     // cu_q_lens[0 .. num_seqs] as read
   int32_t red[3 * kPlanWaves];
 };
 using PlanCore = PlanCoreT<kMaxDecodeSeqs>;
@@ -72,15 +73,19 @@ __device__ __forceinline__ void decode_range(const Params& p, int32_t kv_len, in
 
 // A decode sequence has 1 <= q_len <= dq new tokens (their q_len * qpk rows
 // fit the decode kernel's 16 MFMA columns), inside the token and key ranges.
+// c0, c1 = cu_q_lens[s], cu_q_lens[s + 1]; kv = kv_lens[s].
+__device__ __forceinline__ bool is_decode_seq(const Params& p, int32_t c0, int32_t c1, int32_t kv,
+                                              int32_t* kv_len_out, int32_t* q_len_out) {
+  const int32_t q_len = c1 - c0;
+  const int32_t kv_len = min(kv, p.pps * p.ps);
+  *kv_len_out = kv_len;
+  *q_len_out = q_len;
+  return q_len >= 1 && q_len <= p.dq && kv_len >= q_len && c0 >= 0 && c0 + q_len <= p.T;
+}
 __device__ __forceinline__ bool is_decode_seq(const Params& p, const int32_t* cu,
                                               const int32_t* kv_lens, int32_t s,
                                               int32_t* kv_len_out, int32_t* q_len_out) {
-  const int32_t q_len = cu[s + 1] - cu[s];
-  int32_t kv_len = kv_lens[s];
-  kv_len = min(kv_len, p.pps * p.ps);
-  *kv_len_out = kv_len;
-  *q_len_out = q_len;
-  return q_len >= 1 && q_len <= p.dq && kv_len >= q_len && cu[s] >= 0 && cu[s] + q_len <= p.T;
+  return is_decode_seq(p, cu[s], cu[s + 1], kv_lens[s], kv_len_out, q_len_out);
 }
 
 // In-place exclusive scan of a[0..n) (values >= 0); a[n] = total.
@@ -129,29 +134,47 @@ __device__ __forceinline__ Plan build_plan(const Params& p, const int32_t* kv_le
                                            bool decode_enabled, PlanLds& L, PlanRows* R) {
   Plan pl;
   const int tid = threadIdx.x;
+  // The metadata of every sequence slot below min(S, capacity) is loaded
+  // without waiting for distribution[2]: the two loads are independent, so
+  // the plan costs one memory round trip instead of two.  Slots at or past
+  // num_seqs are then treated as empty.
+  const int32_t n_cap = min(p.S, PlanLds::kCap);
   const int32_t n = min(num_seqs_of(dist, p.S), PlanLds::kCap);
   pl.num_seqs = n;
   int32_t tiles = 0, seqs = 0, others = 0;
   // Wider workgroups (the prefill kernel's 512 threads) take part with their
   // first kPlanThreads threads only: the reduction slots hold kPlanWaves waves.
   const bool planner = tid < kPlanThreads;
-  for (int32_t s = planner ? tid : n; s < n; s += kPlanThreads) {
+  for (int32_t s = planner ? tid : n_cap; s < n_cap; s += kPlanThreads) {
+    const int32_t c0 = cu[s], c1 = cu[s + 1], kv = kv_lens[s];
+    const bool live = s < n;
+    // Always evaluated: kl (the clamped kv_len) feeds the row plan R too.
     int32_t kl, ql;
-    const bool dec = is_decode_seq(p, cu, kv_lens, s, &kl, &ql) && decode_enabled;
+    const bool dseq = is_decode_seq(p, c0, c1, kv, &kl, &ql);
+    const bool dec = live && decode_enabled && dseq;
     const int32_t nt = dec ? decode_tiles(p, kl, ql, tile) : 0;
     seqs += dec ? 1 : 0;
-    others += (!dec && cu[s + 1] > cu[s]) ? 1 : 0;
+    others += (live && !dec && c1 > c0) ? 1 : 0;
     L.dkv[s] = dec ? kl : 0;
     L.ql[s] = dec ? ql : 0;
-    L.tq[s] = min(max(cu[s], 0), max(p.T - 1, 0));
-    L.base[s] = nt;  // scanned into the prefix below
-    if (R != nullptr) {
+    L.tq[s] = min(max(c0, 0), max(p.T - 1, 0));
+    L.cu[s] = c0;
+    L.base[s] = live ? nt : 0;  // scanned into the prefix below
+    if (live && R != nullptr) {
       R->kvlen[s] = kl;
-      R->cu[s] = cu[s];
+      R->cu[s] = c0;
+    }
+    // cu_q_lens[num_seqs]: the end of the last sequence's rows.
+    if (s + 1 == n) {
+      L.cu[n] = c1;
+      if (R != nullptr) R->cu[n] = c1;
     }
     tiles += nt;
   }
-  if (R != nullptr && tid == 0) R->cu[n] = cu[n];
+  if (n == 0 && tid == 0) {
+    L.cu[0] = cu[0];
+    if (R != nullptr) R->cu[0] = L.cu[0];
+  }
   for (int o = 32; o > 0; o >>= 1) {
     tiles += __shfl_xor(tiles, o, 64);
     seqs += __shfl_xor(seqs, o, 64);
@@ -171,7 +194,7 @@ __device__ __forceinline__ Plan build_plan(const Params& p, const int32_t* kv_le
     nother += L.red[2 * kPlanWaves + w];
   }
   pl.n_other = nother;
-  pl.cu_end = cu[n];
+  pl.cu_end = L.cu[n];
   (void)nseq;
   __syncthreads();
   block_exclusive_scan(L.base, n, L.red);
@@ -184,9 +207,11 @@ __device__ __forceinline__ Plan build_plan(const Params& p, const int32_t* kv_le
 
 // Publishes the plan for the finish kernel (every thread of the workgroup
 // takes part; workgroup b writes the row map of sequences b, b + G, ...).
+// The row map takes cu_q_lens from the plan in LDS, so publishing issues
+// stores only and never waits on memory.
 template <typename PlanLds>
 __device__ __forceinline__ void publish_plan(const Params& p, const Plan& pl, const PlanLds& L,
-                                             const int32_t* cu, int32_t* plan) {
+                                             int32_t* plan) {
   const PlanView v = plan_view(plan, p.S);
   int32_t* base = const_cast<int32_t*>(v.base);
   int32_t* dkv = const_cast<int32_t*>(v.dkv);
@@ -209,12 +234,12 @@ __device__ __forceinline__ void publish_plan(const Params& p, const Plan& pl, co
   }
   const int32_t G = static_cast<int32_t>(gridDim.x);
   for (int32_t s = static_cast<int32_t>(blockIdx.x); s < n; s += G) {
-    const int32_t r0 = min(max(cu[s], 0), p.T), r1 = min(max(cu[s + 1], r0), p.T);
+    const int32_t r0 = min(max(L.cu[s], 0), p.T), r1 = min(max(L.cu[s + 1], r0), p.T);
     const int32_t val = L.dkv[s] > 0 ? -1 : s;
     for (int32_t t = r0 + tid; t < r1; t += kPlanThreads) rowseq[t] = val;
   }
   // Padding rows.
-  const int32_t pad0 = min(max(cu[n], 0), p.T);
+  const int32_t pad0 = min(max(L.cu[n], 0), p.T);
   for (int32_t t = pad0 + static_cast<int32_t>(blockIdx.x) * kPlanThreads + tid; t < p.T;
        t += G * kPlanThreads)
     rowseq[t] = -1;
