@@ -219,6 +219,28 @@ def test_nan_poison_isolation(gpu_device):
     assert torch.isfinite(out).all()
 
 
+@pytest.mark.parametrize("qh,kvh,seqs,kv_dtype", [
+    (8, 2, [(1, 129), (1, 2048), (1, 8), (1, 77)], BF16),             # decode kernel only
+    (8, 2, [(1, 300), (17, 80), (1, 33), (40, 41), (1, 1000)], BF16),  # decode + prefill
+    (24, 1, [(17, 80), (1, 300), (5, 18)], BF16),                     # qpk > 16: no decode kernel
+    (32, 8, [(1, 513), (3, 70), (1, 64)], E4M3),
+])
+def test_unused_sequence_slots_are_ignored(gpu_device, qh, kvh, seqs, kv_dtype):
+    """Every kernel's plan loads kv_lens and cu_q_lens of all max_num_seqs
+    slots before it knows num_seqs (distribution[2]); slots past num_seqs must
+    change nothing, whatever they hold (the reference reads only s < num_seqs,
+    kernel.py:1345-1349)."""
+    n = len(seqs)
+    w = W.make_workload(seqs, qh, kvh, 128, 16, kv_dtype=kv_dtype, seed=40 + n,
+                        max_num_seqs=n + 6, name="unused-slots",
+                        **({"k_scale": 0.5, "v_scale": 0.5} if kv_dtype == E4M3 else {}))
+    w.kv_lens[n:] = torch.tensor([1 << 30, -5, 7, 1 << 20, 0, 3], dtype=torch.int32)
+    last = int(w.cu_q_lens[n])
+    w.cu_q_lens[n + 1:] = torch.tensor([last - 3, last + 4096, -1, last + 1, 1 << 29, last],
+                                       dtype=torch.int32)
+    check(w, gpu_device)
+
+
 def test_nan_sequence_stays_in_its_rows(gpu_device):
     w = W.make_workload([(3, 40), (1, 100), (5, 77)], 8, 2, 128, 16, seed=12, name="nanseq")
     S = w.kv_lens.shape[0]
