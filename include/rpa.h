@@ -78,7 +78,10 @@ typedef enum rpa_path {
  *   kv_lens  i32[max_num_seqs], page_indices i32[max_num_seqs * pages_per_seq],
  *   cu_q_lens i32[max_num_seqs + 1], distribution i32[3]
  *   out      [max_num_tokens, num_q_heads, head_dim]           (out_dtype)
- * All tensors are dense row-major. */
+ * All tensors are dense row-major.  The kernels may load every one of the
+ * max_num_seqs entries of kv_lens and cu_q_lens (so all must be allocated);
+ * entries of sequences at or past distribution[2] change nothing, whatever
+ * they hold. */
 typedef struct rpa_desc {
   int32_t abi_version; /* = RPA_ABI_VERSION */
   int32_t q_dtype;     /* rpa_dtype of queries                */
