@@ -9,18 +9,97 @@ import numpy as np
 import torch
 
 
+# ---------------------------------------------------------------------------
+# Number formats, written from their definitions (sign, exponent bits,
+# mantissa bits, bias), for the q_scale branch of the brute force.  None of
+# this calls torch's casts.
+# ---------------------------------------------------------------------------
+# (exponent bits, mantissa bits, bias, has_inf): OCP fp8 e4m3fn has no
+# infinities and only S.1111.111 as NaN; e5m2 is IEEE-like.
+_FP8_FORMATS = {"e4m3fn": (4, 3, 7, False), "e5m2": (5, 2, 15, True)}
+
+
+def fp8_values(fmt: str) -> np.ndarray:
+    """Every finite non-negative value of an fp8 format, ascending (codes
+    0x00..0x7f minus NaN/inf), as float64."""
+    eb, mb, bias, has_inf = _FP8_FORMATS[fmt]
+    vals = []
+    for code in range(1 << (eb + mb)):
+        e, m = code >> mb, code & ((1 << mb) - 1)
+        if e == (1 << eb) - 1 and (has_inf or m == (1 << mb) - 1):
+            continue  # inf / NaN codes
+        if e == 0:
+            vals.append(m * 2.0 ** (1 - bias - mb))
+        else:
+            vals.append((1 + m / 2.0 ** mb) * 2.0 ** (e - bias))
+    return np.array(vals)
+
+
+def round_to_fp8(x: np.ndarray, fmt: str) -> np.ndarray:
+    """Round-to-nearest, ties to the even code (= even mantissa LSB, since the
+    codes are ordered like their magnitudes), of values within the format's
+    range."""
+    vals = fp8_values(fmt)
+    a = np.abs(x)
+    assert (a <= vals[-1]).all(), "value outside the fp8 range (clip first)"
+    hi = np.searchsorted(vals, a, side="left")  # first value >= a
+    hi = np.minimum(hi, len(vals) - 1)
+    lo = np.maximum(hi - 1, 0)
+    dlo, dhi = a - vals[lo], vals[hi] - a
+    pick_hi = (dhi < dlo) | ((dhi == dlo) & (hi % 2 == 0))
+    r = np.where(pick_hi, vals[hi], vals[lo])
+    r = np.where(a == vals[hi], vals[hi], r)
+    return np.sign(x) * r
+
+
+def round_to_bf16(x: np.ndarray) -> np.ndarray:
+    """float32 values -> nearest bf16 (ties to even), via the f32 bit pattern."""
+    u = np.asarray(x, dtype=np.float32).view(np.uint32).astype(np.uint64)
+    u = (u + 0x7FFF + ((u >> 16) & 1)) & 0xFFFF0000
+    return u.astype(np.uint32).view(np.float32).astype(np.float64)
+
+
+def fmt_max(dtype: torch.dtype) -> float:
+    """Largest finite value of a floating format, from its definition."""
+    if dtype == torch.bfloat16:
+        return (2.0 - 2.0 ** -7) * 2.0 ** 127
+    if dtype == torch.float32:
+        return (2.0 - 2.0 ** -23) * 2.0 ** 127
+    return float(fp8_values({torch.float8_e4m3fn: "e4m3fn",
+                             torch.float8_e5m2: "e5m2"}[dtype])[-1])
+
+
+def quantize_q(q: torch.Tensor, q_scale: float, kv_dtype: torch.dtype) -> np.ndarray:
+    """kernel.py:176-183 restated from the definitions: q / q_scale computed in
+    q's dtype (an f32 quotient rounded to bf16 for a bf16 q), clipped to the
+    KV dtype's finite range, then rounded to the KV dtype."""
+    qf = q.to(torch.float64).numpy()
+    quot = (qf.astype(np.float32) / np.float32(q_scale)).astype(np.float64)
+    if q.dtype == torch.bfloat16:
+        quot = round_to_bf16(quot)
+    mx = fmt_max(kv_dtype)
+    quot = np.clip(quot, -mx, mx)
+    if kv_dtype == torch.bfloat16:
+        return round_to_bf16(quot)
+    if kv_dtype == torch.float32:
+        return quot.astype(np.float32).astype(np.float64)
+    return round_to_fp8(quot, {torch.float8_e4m3fn: "e4m3fn", torch.float8_e5m2: "e5m2"}[kv_dtype])
+
+
 def brute_force_rpa(q, k, v, kv_cache, kv_lens, page_indices, cu_q_lens, distribution, *,
                     sm_scale=1.0, sliding_window=None, soft_cap=None, k_scale=None,
-                    v_scale=None, use_causal_mask=True, skip_kv_update=False,
+                    v_scale=None, q_scale=None, use_causal_mask=True, skip_kv_update=False,
                     return_lse=False, attention_sink=None):
     """Per-element fp64 attention written directly from the semantic contract
     (positions, page table, K/V combined-head interleave), independent of the
     oracle's gather/einsum code.  Returns [num_tokens, Hq, D] float64 (and,
     with return_lse, the per-row log(sum_j exp(logit_j)) [num_tokens, Hq]).
     attention_sink [Hq]: one more term exp(sink) in each row's denominator.
+    q_scale (kernel.py:176-183): q is quantized by `quantize_q` and the logit
+    multiplied by q_scale.
     A head_dim 64 packed cache is read through its view
     [P, ps, 2 * heads / pack, pack, 64] (K_h at combined head 2h, V_h at 2h + 1)."""
-    Q = q.to(torch.float64).numpy()
+    Q = q.to(torch.float64).numpy() if q_scale is None else quantize_q(q, q_scale, kv_cache.dtype)
     K = k.to(torch.float64).numpy()
     V = v.to(torch.float64).numpy()
     C = kv_cache.to(torch.float64).numpy()
@@ -59,6 +138,8 @@ def brute_force_rpa(q, k, v, kv_cache, kv_lens, page_indices, cu_q_lens, distrib
                     x = float(np.dot(Q[q0 + i, gq], kr)) * sm_scale
                     if k_scale is not None:
                         x *= k_scale
+                    if q_scale is not None:
+                        x *= q_scale
                     if soft_cap is not None:
                         x = soft_cap * math.tanh(x / soft_cap)
                     logits.append(x)

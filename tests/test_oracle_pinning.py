@@ -183,6 +183,90 @@ def test_oracle_non_causal_vs_bruteforce():
     assert_close(out, bf, 1e-10, 1e-10)
 
 
+# ---------------------------------------------------------------------------
+# q_scale branch (kernel.py:176-183): q / q_scale, clip to the KV dtype's
+# range, cast to the KV dtype; the logits are multiplied by q_scale.
+# ---------------------------------------------------------------------------
+def test_format_tables_from_definitions():
+    """The brute force's own fp8 / bf16 rounding: closed forms of the formats,
+    and agreement with torch's casts on random values (two independent
+    implementations)."""
+    from rpa_testlib import fp8_values, round_to_bf16, round_to_fp8
+
+    e4 = fp8_values("e4m3fn")
+    assert len(e4) == 127 and e4[-1] == 448.0 and e4[1] == 2.0 ** -9
+    e5 = fp8_values("e5m2")
+    assert len(e5) == 124 and e5[-1] == 57344.0 and e5[1] == 2.0 ** -16
+    assert (np.diff(e4) > 0).all() and (np.diff(e5) > 0).all()
+    g = torch.Generator().manual_seed(3)
+    x = torch.randn(20000, generator=g, dtype=torch.float64) * 30
+    for fmt, dt, mx in (("e4m3fn", E4M3, 448.0), ("e5m2", E5M2, 57344.0)):
+        xc = x.clamp(-mx, mx)
+        mine = round_to_fp8(xc.numpy(), fmt)
+        theirs = xc.to(torch.float32).to(dt).to(torch.float64).numpy()
+        assert np.array_equal(mine, theirs), fmt
+    # Ties go to the even code: 1 + 2^-4 sits between 1 and 1.125 in e4m3fn.
+    assert round_to_fp8(np.array([1.0625, 1.1875]), "e4m3fn").tolist() == [1.0, 1.25]
+    xf = x.to(torch.float32)
+    assert np.array_equal(round_to_bf16(xf.numpy()),
+                          xf.to(BF16).to(torch.float64).numpy())
+
+
+Q_SCALE_CASES = [
+    (BF16, 0.37, 1.0),
+    (E4M3, 0.5, 1.0),
+    (E4M3, 0.004, 1.0),   # q / q_scale beyond 448 for |q| > 1.8: the clip matters
+    (E5M2, 0.25, 1.0),
+    (E4M3, 2.0, 40.0),    # large q: clipped after the division
+]
+
+
+@pytest.mark.parametrize("case", range(len(Q_SCALE_CASES)))
+def test_oracle_q_scale_vs_bruteforce(case):
+    kv_dtype, q_scale, q_mul = Q_SCALE_CASES[case]
+    scales = dict(k_scale=0.75, v_scale=1.5) if kv_dtype != BF16 else {}
+    w = wl([(5, 18), (1, 29), (7, 40)], 8, 2, 32, 16, kv_dtype=kv_dtype, seed=61 + case,
+           q_scale=q_scale, **scales)
+    w.q.mul_(q_mul)
+    out, _ = O.ref_ragged_paged_attention(*w.args(), mode="fp64", **w.kwargs)
+    bf = brute_force_rpa(*w.args(), **w.kwargs)
+    assert_close(out, bf, 1e-10, 1e-10, "fp64 oracle vs brute force, q_scale")
+    out32, _ = O.ref_ragged_paged_attention(*w.args(), mode="fp32", **w.kwargs)
+    assert_close(out32, bf, 1e-5, 1e-5, "fp32 oracle vs brute force, q_scale")
+
+
+@pytest.mark.parametrize("mistake", ["no_multiply_back", "no_clip", "no_cast"])
+def test_q_scale_pin_catches_planted_mistakes(mistake):
+    """Slips of the q_scale branch, planted in the oracle's inputs on the CPU,
+    move its result far from the brute force (the pin above holds to 1e-10)."""
+    from rpa_testlib import round_to_bf16
+
+    kv_dtype, q_scale, q_mul = (E4M3, 0.004, 1.0) if mistake != "no_cast" else (E4M3, 0.5, 1.0)
+    w = wl([(5, 18), (1, 29), (7, 40)], 8, 2, 32, 16, kv_dtype=kv_dtype, seed=71,
+           q_scale=q_scale, k_scale=0.75, v_scale=1.5)
+    w.q.mul_(q_mul)
+    bf = brute_force_rpa(*w.args(), **w.kwargs)
+    args, kw = list(w.args()), dict(w.kwargs)
+    qd = torch.from_numpy(round_to_bf16((w.q.float() / q_scale).numpy()))
+    if mistake == "no_multiply_back":
+        # q quantized as the reference does, logits never multiplied by q_scale.
+        args[0] = qd.clamp(-448, 448).to(E4M3).to(torch.float64)
+        kw.pop("q_scale")
+    elif mistake == "no_clip":
+        # Out-of-range quotients left unclipped (carried at full precision).
+        args[0] = qd.to(torch.float64)
+        kw.pop("q_scale")
+        kw["k_scale"] = kw["k_scale"] * q_scale
+    else:
+        # q never rounded to the KV dtype.
+        args[0] = qd.to(torch.float64)
+        kw.pop("q_scale")
+        kw["k_scale"] = kw["k_scale"] * q_scale
+    out, _ = O.ref_ragged_paged_attention(*args, mode="fp64", validate=False, **kw)
+    n = bf.shape[0]
+    assert (out[:n] - bf).abs().max().item() > 1e-3, mistake
+
+
 def _sdpa(q, k, v, causal, scale):
     # q [L, H, D], k/v [S, H, D] -> [L, H, D], fp64
     o = torch.nn.functional.scaled_dot_product_attention(

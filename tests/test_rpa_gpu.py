@@ -14,7 +14,7 @@ import pytest
 import torch
 
 from oracle import rpa_oracle as O
-from rpa_testlib import assert_close, bytes_equal
+from rpa_testlib import assert_close, bytes_diff, bytes_equal
 
 import vllm_torchtpu_amd as R
 import vllm_torchtpu_amd.workloads as W
@@ -253,14 +253,22 @@ def test_nan_sequence_stays_in_its_rows(gpu_device):
 
 
 def test_bundled_matches_flat(gpu_device):
-    """test_rpa_bundled.py:173-227: bundled block-major == per-layer flat, bitwise."""
+    """test_rpa_bundled.py:173-227: bundled block-major == per-layer flat, bitwise;
+    and both equal the oracle on that layer (kernel.py:2011-2061: logical page p
+    of layer l is flat page p * num_layers + l, updated in place)."""
     layers, P = 3, 96
     w = W.make_workload([(1, 128)] * 4 + [(32, 192)] * 4, 16, 4, 128, 16, seed=13,
                         num_pages=P, distribution=[4, 8, 8], name="bundled")
     g = torch.Generator().manual_seed(0)
     init = torch.randn(layers, *w.kv_cache.shape, generator=g).to(BF16)
     dev = gpu_device
+    n = w.num_tokens
     for layer in range(layers):
+        # The oracle on this layer's flat cache: the bundle's pages p * layers +
+        # layer are exactly init[layer][p].
+        args = list(w.args())
+        args[3] = init[layer].clone()
+        exp_out, exp_cache = O.ref_ragged_paged_attention(*args, mode="fp32", **w.kwargs)
         flat = w.to(dev)
         flat_cache = init[layer].clone().to(dev)
         out_ref, _ = R.ragged_paged_attention(flat.q, flat.k, flat.v, flat_cache, flat.kv_lens,
@@ -271,9 +279,11 @@ def test_bundled_matches_flat(gpu_device):
             flat.q, flat.k, flat.v, bundle, layer, flat.kv_lens, flat.page_indices,
             flat.cu_q_lens, flat.distribution, **w.kwargs)
         torch.cuda.synchronize()
-        n = w.num_tokens
         assert bytes_equal(out_ref[:n].cpu(), out_b[:n].cpu())
         assert bytes_equal(flat_cache.cpu(), bundle[:, layer].cpu())
+        assert_close(out_b[:n], exp_out[:n], 2e-2, 2e-2, f"bundled layer {layer} vs oracle")
+        assert bytes_equal(bundle[:, layer].cpu(), exp_cache), \
+            bytes_diff(bundle[:, layer].cpu(), exp_cache)
         others = [x for x in range(layers) if x != layer]
         assert bytes_equal(bundle[:, others].cpu(), init.transpose(0, 1)[:, others].contiguous())
 
