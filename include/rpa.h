@@ -55,6 +55,7 @@ typedef enum rpa_status {
   RPA_ERR_LAUNCH = -4,       /* a HIP launch failed                            */
   RPA_ERR_NULL_PTR = -5,     /* a required pointer is NULL                     */
   RPA_ERR_ABI = -6,          /* descriptor abi_version mismatch                */
+  RPA_ERR_SCRATCH = -7,      /* rpa_forward_noalloc: needs more than its scratch */
 } rpa_status;
 
 /* Kernel-path selection (rpa_desc.path). */
@@ -202,6 +203,27 @@ int rpa_forward_ex(const rpa_desc* d, const void* queries, const void* keys,
 int rpa_merge_attn_states(int32_t num_parts, int64_t rows, int32_t head_dim, int32_t dtype,
                           const void* outs, const float* lses, void* out, float* lse_out,
                           void* stream);
+
+/* Size of rpa_forward_noalloc's fixed device scratch (per GPU). */
+#define RPA_NOALLOC_SCRATCH_BYTES ((size_t)32 << 20)
+
+/* rpa_forward without a workspace argument: the same kernels, with the decode
+ * partials and work plan in a fixed RPA_NOALLOC_SCRATCH_BYTES device buffer
+ * that the library holds per GPU (a static device array; each GPU it runs on
+ * keeps its own copy until the process ends).  It allocates nothing: no
+ * hipMalloc, hipFree or allocating library call, ever.  No counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * Returns RPA_ERR_SCRATCH when rpa_workspace_size(d) exceeds
+ * RPA_NOALLOC_SCRATCH_BYTES (call rpa_forward with a workspace then).  Every
+ * call on one GPU shares that GPU's buffer, so calls that overlap on one GPU
+ * (different streams, or different host threads without ordering) race;
+ * calls ordered on one stream are safe.  Nothing in the buffer needs
+ * clearing between calls. */
+int rpa_forward_noalloc(const rpa_desc* d, const void* queries, const void* keys,
+                        const void* values, void* kv_cache, const int32_t* kv_lens,
+                        const int32_t* page_indices, const int32_t* cu_q_lens,
+                        const int32_t* distribution, void* out, void* stream);
 
 #ifdef __cplusplus
 }

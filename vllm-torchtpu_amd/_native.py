@@ -31,6 +31,10 @@ RPA_ERR_WORKSPACE = -3
 RPA_ERR_LAUNCH = -4
 RPA_ERR_NULL_PTR = -5
 RPA_ERR_ABI = -6
+RPA_ERR_SCRATCH = -7
+
+# Fixed per-GPU scratch of rpa_forward_noalloc (RPA_NOALLOC_SCRATCH_BYTES).
+NOALLOC_SCRATCH_BYTES = 32 << 20
 
 RPA_PATH_AUTO = 0
 RPA_PATH_GENERIC = 1
@@ -56,6 +60,7 @@ EXPORTED_SYMBOLS = (
     "rpa_forward_lse",
     "rpa_forward_ex",
     "rpa_merge_attn_states",
+    "rpa_forward_noalloc",
 )
 
 
@@ -130,6 +135,8 @@ def lib() -> ctypes.CDLL:
     L.rpa_forward_lse.argtypes = [desc_p] + [P] * 11 + [ctypes.c_size_t, P]
     L.rpa_forward_ex.restype = ctypes.c_int
     L.rpa_forward_ex.argtypes = [desc_p] + [P] * 12 + [ctypes.c_size_t, P]
+    L.rpa_forward_noalloc.restype = ctypes.c_int
+    L.rpa_forward_noalloc.argtypes = [desc_p] + [P] * 10
     L.rpa_merge_attn_states.restype = ctypes.c_int
     L.rpa_merge_attn_states.argtypes = [ctypes.c_int32, ctypes.c_int64, ctypes.c_int32,
                                         ctypes.c_int32, P, P, P, P, P]

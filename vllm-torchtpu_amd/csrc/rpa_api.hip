@@ -5,6 +5,8 @@
 #include <math.h>
 #include <string.h>
 
+#include <mutex>
+
 #include "rpa.h"
 #include "rpa_common.h"
 #include "rpa_internal.h"
@@ -86,6 +88,38 @@ int current_num_cus() {
 
 }  // namespace
 
+// Scratch of rpa_forward_noalloc: the decode partials and the published plan
+// that rpa_forward keeps in the caller's workspace.  Each GPU the library runs
+// on holds its own copy of this array until the process ends.  In host code
+// the name is a host-side stand-in, never a device address: host code uses
+// only the per-device address hipGetSymbolAddress returns (g_scratch_dev).
+static __device__ __align__(256) unsigned char scratch[RPA_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_dev[kMaxDevices] = {};
+
+// Device address of the current device's copy of `scratch`, looked up once per
+// device (with that device current) on its first rpa_forward_noalloc call.
+int scratch_of_current_device(void** ptr) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess) return RPA_ERR_LAUNCH;
+  if (dev < 0 || dev >= kMaxDevices) return RPA_ERR_UNSUPPORTED;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_dev[dev] == nullptr) {
+    void* p = nullptr;
+    if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || p == nullptr)
+      return RPA_ERR_LAUNCH;
+    g_scratch_dev[dev] = p;
+  }
+  *ptr = g_scratch_dev[dev];
+  return RPA_OK;
+}
+
+}  // namespace
+
 extern "C" {
 
 int rpa_abi_version(void) { return RPA_ABI_VERSION; }
@@ -99,6 +133,9 @@ const char* rpa_status_str(int status) {
     case RPA_ERR_LAUNCH: return "HIP kernel launch failed";
     case RPA_ERR_NULL_PTR: return "a required device pointer is NULL";
     case RPA_ERR_ABI: return "rpa_desc.abi_version does not match the library";
+    case RPA_ERR_SCRATCH:
+      return "the call needs more scratch than rpa_forward_noalloc's fixed buffer "
+             "(RPA_NOALLOC_SCRATCH_BYTES); call rpa_forward with a workspace instead";
     default: return "unknown status";
   }
 }
@@ -260,6 +297,25 @@ int rpa_forward_ex(const rpa_desc* d, const void* queries, const void* keys, con
                                     kv_cache, kv_lens, page_indices, cu_q_lens, distribution, out,
                                     cus, s);
   return e == hipSuccess ? RPA_OK : RPA_ERR_LAUNCH;
+}
+
+int rpa_forward_noalloc(const rpa_desc* d, const void* queries, const void* keys,
+                        const void* values, void* kv_cache, const int32_t* kv_lens,
+                        const int32_t* page_indices, const int32_t* cu_q_lens,
+                        const int32_t* distribution, void* out, void* stream) {
+  const int st = rpa_validate_desc(d);
+  if (st != RPA_OK) return st;
+  const size_t need = rpa_workspace_size(d);
+  if (need > RPA_NOALLOC_SCRATCH_BYTES) return RPA_ERR_SCRATCH;
+  if (d->max_num_tokens == 0) return RPA_OK;
+  void* ws = nullptr;
+  const int sst = scratch_of_current_device(&ws);
+  if (sst != RPA_OK) return sst;
+  // The same kernels as rpa_forward, on this device's scratch (nothing in it
+  // needs clearing: the kernels write every slot before reading it).
+  return rpa_forward_ex(d, queries, keys, values, kv_cache, kv_lens, page_indices, cu_q_lens,
+                        distribution, out, nullptr, nullptr, ws, RPA_NOALLOC_SCRATCH_BYTES,
+                        stream);
 }
 
 }  // extern "C"
