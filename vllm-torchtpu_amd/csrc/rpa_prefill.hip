@@ -606,6 +606,8 @@ prefill_kernel(Params p, const uint16_t* __restrict__ q,
     }
 }
 
+#include "rpa_prefill_dma.h"
+
 template <typename KV, typename OutS>
 hipError_t launch_dp(const Params& p, const void* q, const void* k, const void* v, void* cache,
                      const int32_t* kv_lens, const int32_t* page_indices, const int32_t* cu,
@@ -629,6 +631,20 @@ hipError_t launch_dp(const Params& p, const void* q, const void* k, const void* 
                      page_indices, cu, dist, static_cast<OutS*>(out), ws.plan, ws.part_o,    \
                      ws.part_ml, nfm, nfw)
   const bool full = p.D == p.Dp;
+  if constexpr (sizeof(E) == 2) {
+    // bf16 KV at head_dim 128: the LDS-DMA kernel (rpa_prefill_dma.h).
+    if (p.Dp == 128 && full) {
+#define RPA_DMA_LAUNCH(CAP)                                                                    \
+  hipLaunchKernelGGL((prefill_dma_kernel<OutS, CAP>), g, dim3(DmaCfg::THREADS), 0, stream, p,  \
+                     static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k),          \
+                     static_cast<const uint16_t*>(v), static_cast<uint16_t*>(cache), kv_lens,   \
+                     page_indices, cu, dist, static_cast<OutS*>(out), ws.plan, ws.part_o,       \
+                     ws.part_ml, nfm, nfw)
+      if (p.has_cap) RPA_DMA_LAUNCH(true); else RPA_DMA_LAUNCH(false);
+#undef RPA_DMA_LAUNCH
+      return hipGetLastError();
+    }
+  }
   if (p.Dp == 64) {
     if (full) RPA_PREFILL_LAUNCH(64, true); else RPA_PREFILL_LAUNCH(64, false);
   } else if (p.Dp == 128) {

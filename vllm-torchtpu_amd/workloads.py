@@ -159,6 +159,32 @@ def make_workload(seq_lens, num_q_heads, num_kv_heads, head_dim, page_size, *,
                     list(seq_lens))
 
 
+def prefill_part(w: Workload) -> Workload:
+    """The sequences of `w` with more than one query token, alone: the same
+    cache, the same page-table rows, distribution [0, 0, n] (the prefill
+    kernel's share of a mixed batch, timed by itself)."""
+    S = w.kv_lens.shape[0]
+    pps = w.page_indices.shape[0] // S
+    n = w.num_seqs
+    keep = [s for s in range(n) if int(w.cu_q_lens[s + 1]) - int(w.cu_q_lens[s]) > 1]
+    m = len(keep)
+    cu = torch.zeros(m + 1, dtype=torch.int32)
+    kvl = torch.zeros(m, dtype=torch.int32)
+    pages = torch.empty(m * pps, dtype=torch.int32)
+    rows = []
+    for i, s in enumerate(keep):
+        c0, c1 = int(w.cu_q_lens[s]), int(w.cu_q_lens[s + 1])
+        cu[i + 1] = cu[i] + (c1 - c0)
+        kvl[i] = w.kv_lens[s]
+        pages[i * pps:(i + 1) * pps] = w.page_indices[s * pps:(s + 1) * pps]
+        rows.append(torch.arange(c0, c1))
+    idx = torch.cat(rows) if rows else torch.zeros(0, dtype=torch.int64)
+    return Workload(w.name + "-prefill", w.q[idx].contiguous(), w.k[idx].contiguous(),
+                    w.v[idx].contiguous(), w.kv_cache, kvl, pages, cu,
+                    torch.tensor([0, 0, m], dtype=torch.int32), dict(w.kwargs),
+                    [w.seq_lens[s] for s in keep])
+
+
 def _uniform_ints(g, lo, hi, n):
     return torch.randint(lo, hi + 1, (n,), generator=g).tolist()
 
