@@ -55,8 +55,11 @@ def _log(msg):
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
-def cpu_baseline(w, seconds):
-    """Time the CPU oracle (faithful mode) on the same workload."""
+def cpu_baseline(w, seconds, call_bytes):
+    """Time the CPU oracle (faithful mode, a restatement of the reference's
+    ref_ragged_paged_attention) on the same workload: whole calls, the median
+    of up to 5 within `seconds` (at least one).  Reports query tokens/s and
+    the algorithmic GB/s of those calls."""
     import torch
 
     from oracle import rpa_oracle as O
@@ -75,7 +78,6 @@ def cpu_baseline(w, seconds):
                 break
     except OSError:
         pass
-    O.ref_ragged_paged_attention(*w.args(), mode="faithful", validate=False, **w.kwargs)
     times = []
     t_start = time.perf_counter()
     while len(times) < 5 and (time.perf_counter() - t_start < seconds or len(times) < 1):
@@ -86,10 +88,11 @@ def cpu_baseline(w, seconds):
     return {
         "value": w.num_tokens / med,
         "unit": "tokens/s",
+        "gbps": round(call_bytes / med / 1e9, 3),
         "cores": torch.get_num_threads(),
         "kind": "port",
         "sample": (f"full workload ({w.num_seqs} seqs, {w.num_tokens} query tokens) per call; "
-                   f"median of {len(times)} calls after 1 warm-up; {med * 1e3:.1f} ms/call; "
+                   f"median of {len(times)} calls; {med * 1e3:.1f} ms/call; "
                    f"oracle faithful mode (torch CPU) on {model}"),
     }
 
@@ -215,7 +218,7 @@ def main():
         torch.cuda.synchronize()
         return e0.elapsed_time(e1) / args.steps
 
-    graph_s = attn_ms = kern_ms = None
+    graph_s = attn_ms = kern_ms = median_step_ms = None
     if not args.no_graph:
         _log("capturing HIP graphs")
         fns = [step, attn_only] + ([decode_only] if has_decode else [])
@@ -243,6 +246,17 @@ def main():
             graphs[0].replay()
         torch.cuda.synchronize()
         graph_s = time.perf_counter() - t0
+        # Per-step times of graph replays (HIP events around each one).
+        per = []
+        for _ in range(args.steps):
+            e0 = torch.cuda.Event(enable_timing=True)
+            e1 = torch.cuda.Event(enable_timing=True)
+            e0.record()
+            graphs[0].replay()
+            e1.record()
+            per.append((e0, e1))
+        torch.cuda.synchronize()
+        median_step_ms = statistics.median(a.elapsed_time(b) for a, b in per)
         attn_ms = replay_ms(graphs[1])
         kern_ms = replay_ms(graphs[2]) if has_decode else attn_ms
 
@@ -285,10 +299,50 @@ def main():
                     "attention_call_ms": round(attn_ms, 5),
                     "attention_call_bytes": attn_bytes}
 
+    # MFMA roofline of the prefill rows: the prefill kernel's share of the
+    # batch (the sequences with more than one query token) timed alone as
+    # graph replays, and its share of the whole attention call (the call
+    # minus the decode kernel alone).
+    roofline_mfma = None
+    if flops > 0 and not args.no_graph:
+        pw = W.prefill_part(w)
+        pg = pw.to(dev)
+        pkw = dict(pw.kwargs)
+
+        def prefill_only():
+            return R.ragged_paged_attention(*pg.args(), skip_kv_update=True, **pkw)
+
+        s2 = torch.cuda.Stream(dev)
+        s2.wait_stream(torch.cuda.current_stream(dev))
+        with torch.cuda.stream(s2):
+            for _ in range(3):
+                prefill_only()
+        torch.cuda.current_stream(dev).wait_stream(s2)
+        torch.cuda.synchronize()
+        pgr = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(pgr):
+            prefill_only()
+        for _ in range(3):
+            pgr.replay()
+        torch.cuda.synchronize()
+        alone_ms = replay_ms(pgr)
+        in_call_ms = attn_ms - kern_ms if has_decode else attn_ms
+        achieved = flops / (alone_ms * 1e-3) / 1e12
+        roofline_mfma = {
+            "bound": "mfma", "achieved": round(achieved, 1), "peak": BF16_PEAK_TFLOPS,
+            "unit": "TFLOP/s", "frac": round(achieved / BF16_PEAK_TFLOPS, 4),
+            "traffic": None, "kernel": "prefill_kernel",
+            "flops_per_launch": flops, "alone_ms": round(alone_ms, 5),
+            "in_call_ms": round(in_call_ms, 5),
+            "in_call_frac": round(flops / (in_call_ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, 4),
+            "note": ("alone: the batch's multi-token sequences by themselves (distribution "
+                     "[0, 0, n]); in_call: attention call minus the decode kernel alone"),
+        }
+
     cpu = None
     if not args.no_cpu_baseline:
         _log("timing CPU oracle baseline")
-        cpu = cpu_baseline(w, args.cpu_seconds)
+        cpu = cpu_baseline(w, args.cpu_seconds, call_bytes)
 
     line = {
         "metric": "RPA tokens/s + achieved HBM GB/s (% of 8 TB/s), Llama-3-8B-shape decode batch",
@@ -311,8 +365,10 @@ def main():
         "timing": timing,
         "eager_ms_per_step": round(eager_s / args.steps * 1e3, 5),
         "graph_ms_per_step": None if graph_s is None else round(graph_s / args.steps * 1e3, 5),
+        "median_graph_step_ms": None if median_step_ms is None else round(median_step_ms, 5),
         "prefill_flops": flops,
         "roofline": roofline,
+        "roofline_mfma": roofline_mfma,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)

@@ -195,14 +195,16 @@ int rpa_forward_ex(const rpa_desc* d, const void* queries, const void* keys,
 /* LSE-weighted merge of num_parts partial attentions of the same rows:
  * outs [num_parts, rows, head_dim] and lses [num_parts, rows] (f32, natural
  * log) -> out [rows, head_dim] and, when lse_out is not NULL, lse_out [rows].
- * dtype (RPA_DTYPE_BF16 or RPA_DTYPE_F32) is that of outs and out; head_dim
- * <= 512.  Replaces merge_attn_results,
+ * dtype (RPA_DTYPE_BF16 or RPA_DTYPE_F32) is that of outs, out_dtype that of
+ * out (the reference returns f32: its f32 weights promote bf16 partials);
+ * head_dim <= 512.  Replaces merge_attn_results,
  *   src/vllm_torchtpu/layers/adapter/cp_attention.py:45-72
- * (exactly, for num_parts = 2; NaN and +-inf partial outputs count as 0) and
- * the local combine of cp_lse_ag_out_rs, distributed/dcp_comm.py:23-68. */
+ * (exactly, for num_parts = 2: NaN and +-inf partial outputs count as 0, a NaN
+ * lse propagates through the max as torch.maximum does) and the local
+ * combine of cp_lse_ag_out_rs, distributed/dcp_comm.py:23-68. */
 int rpa_merge_attn_states(int32_t num_parts, int64_t rows, int32_t head_dim, int32_t dtype,
-                          const void* outs, const float* lses, void* out, float* lse_out,
-                          void* stream);
+                          int32_t out_dtype, const void* outs, const float* lses, void* out,
+                          float* lse_out, void* stream);
 
 /* Size of rpa_forward_noalloc's fixed device scratch (per GPU). */
 #define RPA_NOALLOC_SCRATCH_BYTES ((size_t)32 << 20)

@@ -82,8 +82,12 @@ def _run(head_size, pool_heads, pool_head_size, *, kv_cache_dtype="bf16", two_d=
     key = torch.randn(q_len, num_kv_heads * head_size).to(BF16)
     seen = {}
 
-    def fake_kernel(kv, q, k, v, seq_lens, block_tables, qsl, dist, sink):
-        seen.update(q=q, k=k, v=v, sink=sink)
+    def fake_kernel(kv, q, k, v, seq_lens, block_tables, qsl, dist, sink, out=None):
+        seen.update(q=q, k=k, v=v, sink=sink, direct=out is not None)
+        if out is not None:  # the kernel writes the caller's buffer
+            assert out.shape == q.shape and out.dtype == q.dtype
+            out.fill_(2)
+            return out
         return torch.ones_like(q) * 2
     built = {}
 
@@ -117,9 +121,16 @@ def test_forward_query_width_and_layout():
     out, _, seen, _, q = _run(128, 4, 256)
     assert seen["q"].shape == (3, 4, 256) and out.shape == q.shape
     assert torch.equal(seen["q"][..., 128:], torch.zeros_like(seen["q"][..., 128:]))
-    # 3-D in, 3-D out; the output buffer is written in place.
-    out, buf, _, _, q = _run(128, 4, 128, two_d=False, out_buf=True)
-    assert out.shape == q.shape and torch.equal(buf, out)
+    # 3-D in, 3-D out; the output buffer is written in place, by the kernel
+    # itself (no temporary and copy) when no head padding is involved.
+    out, buf, seen, _, q = _run(128, 4, 128, two_d=False, out_buf=True)
+    assert out.shape == q.shape and torch.equal(buf, out) and seen["direct"]
+    assert out.data_ptr() == buf.data_ptr()
+    out, buf, seen, _, q = _run(128, 4, 128, two_d=True, out_buf=True)
+    assert out.data_ptr() == buf.data_ptr() and seen["direct"] and torch.equal(buf, out)
+    # A padded pool page: the kernel writes a temporary, then the slice is copied.
+    out, buf, seen, _, q = _run(128, 4, 256, two_d=True, out_buf=True)
+    assert not seen["direct"] and torch.equal(buf, out)
 
 
 def test_forward_quantize_on_write():
@@ -173,3 +184,25 @@ def test_sinks_routing():
     with pytest.raises(NotImplementedError, match="head_dim==64"):
         kernel(None, q, q[:, :2], q[:, :2], None, torch.zeros(1, dtype=torch.int32), None,
                None, impl.sinks)
+
+
+def test_workspace_is_never_freed_and_not_grown_in_capture(monkeypatch):
+    """A captured graph keeps the workspace pointer of its calls: a larger
+    workspace replaces the old one for later calls but the old one stays
+    alive, and growing during a capture raises (rpa.py _workspace)."""
+    from vllm_torchtpu_amd import rpa
+
+    dev = torch.device("cpu")
+    monkeypatch.setattr(rpa, "_WORKSPACES", {})
+    monkeypatch.setattr(rpa, "_RETIRED", [])
+    a = rpa._workspace(dev, 100)
+    assert rpa._workspace(dev, 50) is a
+    b = rpa._workspace(dev, 1000)
+    assert b is not a and b.numel() >= 1000 and any(x is a for x in rpa._RETIRED)
+    monkeypatch.setattr(torch.cuda, "is_current_stream_capturing", lambda: True)
+    cuda_dev = torch.device("cuda", 0)
+    monkeypatch.setitem(rpa._WORKSPACES, rpa._ws_key(cuda_dev), b)
+    assert rpa._workspace(cuda_dev, 1000) is b        # no growth: fine under capture
+    with pytest.raises(RuntimeError, match="graph capture"):
+        rpa._workspace(cuda_dev, 10 ** 6)
+

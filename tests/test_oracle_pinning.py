@@ -175,6 +175,16 @@ def test_oracle_vs_bruteforce(case, kv_dtype):
     assert_close(out32, bf, 1e-5, 1e-5, "fp32 oracle vs brute force")
 
 
+def test_oracle_f16_vs_bruteforce():
+    c = dict(BRUTE_CASES[4])
+    seq_lens, hq, hkv, d, ps = (c.pop(x) for x in ("seq_lens", "hq", "hkv", "d", "ps"))
+    w = wl(seq_lens, hq, hkv, d, ps, q_dtype=torch.float16, kv_dtype=torch.float16, seed=17,
+           **c)
+    out, cache = O.ref_ragged_paged_attention(*w.args(), mode="fp64", **w.kwargs)
+    assert cache.dtype == torch.float16
+    assert_close(out, brute_force_rpa(*w.args(), **w.kwargs), 1e-10, 1e-10, "f16")
+
+
 def test_oracle_non_causal_vs_bruteforce():
     w = wl([(5, 18), (3, 7)], 4, 2, 32, 8, seed=5)
     out, _ = O.ref_ragged_paged_attention(*w.args(), mode="fp64", use_causal_mask=False,
@@ -586,3 +596,19 @@ def test_merge_closed_forms():
     # Both partials empty: output 0, lse -inf.
     o, l = O.merge_attn_results(out_b, lse_b, out_b, lse_b)
     assert torch.equal(o, torch.zeros_like(o)) and bool(torch.isneginf(l).all())
+
+
+def test_merge_nan_lse_propagates():
+    """merge_attn_results takes the max with torch.maximum, which propagates a
+    NaN lse (cp_attention.py:59): that row's output and lse are NaN; other
+    rows are untouched."""
+    out_a = torch.ones(3, 1, 4)
+    out_b = torch.full((3, 1, 4), 2.0)
+    lse_a = torch.tensor([[0.0], [float("nan")], [1.0]])
+    lse_b = torch.tensor([[0.0], [0.0], [float("nan")]])
+    o, l = O.merge_attn_results(out_a, lse_a, out_b, lse_b)
+    assert torch.isnan(l[1:]).all() and torch.isnan(o[1:]).all()
+    assert torch.allclose(o[0], torch.full((1, 4), 1.5)) and abs(float(l[0, 0]) - math.log(2)) < 1e-6
+    o3, l3 = O.merge_attn_states(torch.stack([out_a, out_b]), torch.stack([lse_a, lse_b]))
+    assert torch.equal(torch.isnan(o3), torch.isnan(o)) and torch.equal(torch.isnan(l3), torch.isnan(l))
+

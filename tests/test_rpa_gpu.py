@@ -23,7 +23,7 @@ from vllm_torchtpu_amd import _native as N
 pytestmark = pytest.mark.gpu
 
 BF16, E4M3, E5M2 = torch.bfloat16, torch.float8_e4m3fn, torch.float8_e5m2
-TOL = {BF16: 2e-2, E4M3: 5e-2, E5M2: 5e-2, torch.float32: 2e-2}
+TOL = {BF16: 2e-2, E4M3: 5e-2, E5M2: 5e-2, torch.float32: 2e-2, torch.float16: 2e-2}
 
 
 def _log(msg):
@@ -190,6 +190,15 @@ def test_q_scale(gpu_device, dt):
 def test_f32(gpu_device):
     check(W.make_workload(MIXED16, 32, 8, 128, 16, q_dtype=torch.float32,
                           kv_dtype=torch.float32, seed=3, name="f32"), gpu_device)
+
+
+@pytest.mark.parametrize("seqs", [MIXED16, DECODE16])
+def test_f16(gpu_device, seqs):
+    """f16 queries and KV (kernel.py:1447-1453 accepts any float KV dtype): the
+    shape-generic kernels, f16 output."""
+    n = len(seqs)
+    check(W.make_workload(seqs, 32, 8, 128, 16, q_dtype=torch.float16, kv_dtype=torch.float16,
+                          seed=4, distribution=[0, 0, n], name="f16"), gpu_device)
 
 
 def test_non_causal(gpu_device):
@@ -434,16 +443,31 @@ def test_merge_attn_states_gpu(gpu_device, parts, dt):
     lses[0, :5] = float("-inf")          # empty partials
     outs[0, :5] = float("nan")           # ... whose outputs are garbage
     lses[:, 7] = float("-inf")           # a row with no keys anywhere
+    lses[parts - 1, 9, 2] = float("nan")  # a NaN lse propagates (torch.maximum)
     exp_out, exp_lse = O.merge_attn_states(outs.double(), lses.double())
     out, lse = R.merge_attn_states(outs.to(gpu_device), lses.to(gpu_device))
     torch.cuda.synchronize()
-    tol = 2e-2 if dt == BF16 else 1e-5
-    assert_close(out.cpu(), exp_out, tol, tol, "merged output")
-    assert_close(lse.cpu(), exp_lse, 1e-5, 1e-5, "merged lse")
+    assert out.dtype == torch.float32  # the reference's result dtype
+    out, lse = out.cpu(), lse.cpu()
+    nan_o, nan_l = torch.isnan(exp_out), torch.isnan(exp_lse)
+    assert nan_l[9, 2] and nan_o[9, 2].all()
+    assert torch.equal(torch.isnan(out), nan_o) and torch.equal(torch.isnan(lse), nan_l)
+    assert_close(out[~nan_o], exp_out[~nan_o], 1e-5, 1e-5, "merged output")
+    assert_close(lse[~nan_l], exp_lse[~nan_l], 1e-5, 1e-5, "merged lse")
+    # bf16 output: the same values rounded.
+    ob, lb = R.merge_attn_states(outs.to(gpu_device), lses.to(gpu_device),
+                                 out_dtype=torch.bfloat16)
+    torch.cuda.synchronize()
+    assert ob.dtype == BF16
+    assert bytes_equal(ob.cpu()[~nan_o], out[~nan_o].to(BF16))
     if parts == 2:
         o2, l2 = R.merge_attn_results(outs[0].to(gpu_device), lses[0].to(gpu_device),
                                       outs[1].to(gpu_device), lses[1].to(gpu_device))
-        assert torch.equal(o2.cpu(), out.cpu()) and torch.equal(l2.cpu(), lse.cpu())
+        assert torch.equal(o2.cpu().nan_to_num(), out.nan_to_num())
+        assert torch.equal(l2.cpu().nan_to_num(), lse.nan_to_num())
+        ref_o, ref_l = O.merge_attn_results(outs[0].double(), lses[0].double(),
+                                            outs[1].double(), lses[1].double())
+        assert torch.equal(torch.isnan(ref_o), nan_o) and torch.equal(torch.isnan(ref_l), nan_l)
 
 
 def test_dcp_split_merge_equals_full(gpu_device):

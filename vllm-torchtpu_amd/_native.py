@@ -139,7 +139,7 @@ def lib() -> ctypes.CDLL:
     L.rpa_forward_noalloc.argtypes = [desc_p] + [P] * 10
     L.rpa_merge_attn_states.restype = ctypes.c_int
     L.rpa_merge_attn_states.argtypes = [ctypes.c_int32, ctypes.c_int64, ctypes.c_int32,
-                                        ctypes.c_int32, P, P, P, P, P]
+                                        ctypes.c_int32, ctypes.c_int32, P, P, P, P, P]
     if L.rpa_abi_version() != ABI_VERSION:
         raise NativeLibraryMissing(
             f"librpa_hip.so ABI {L.rpa_abi_version()} != expected {ABI_VERSION}; rebuild it")

@@ -226,6 +226,7 @@ class RpaAttentionBackendImpl:
             self.kv_cache_quantized_dtype = STR_DTYPE_TO_TORCH_DTYPE[
                 kv_cache_dtype.lower().strip()]
         self._kernel_config_cache: dict = {}
+        self._shared_kv_zeros: dict = {}
 
     def process_weights_after_loading(self, act_dtype: torch.dtype) -> None:
         """attention.py:1455-1463: the kernels take f32 sinks."""
@@ -245,7 +246,7 @@ class RpaAttentionBackendImpl:
             return fn
 
         def rpa_kernel_impl(kv_cache, query, key_t, value, seq_lens, block_tables,
-                            query_start_loc, request_distribution, sink):
+                            query_start_loc, request_distribution, sink, out=None):
             # head_dim 64 goes to the hd64 kernel, strict window
             # (attention_interface.py:418-436); only it takes sinks.
             if query.shape[-1] == 64:
@@ -267,7 +268,7 @@ class RpaAttentionBackendImpl:
                 skip_kv_update=skip_kv_update, sm_scale=self.scale,
                 sliding_window=self.sliding_window, soft_cap=self.logits_soft_cap,
                 q_scale=q_scale, k_scale=k_scale, v_scale=v_scale,
-                decode_query_size=self.decode_query_size)
+                decode_query_size=self.decode_query_size, out=out)
             return out
 
         self._kernel_config_cache[key] = rpa_kernel_impl
@@ -296,9 +297,14 @@ class RpaAttentionBackendImpl:
             q_len, q_compute_dim = query.shape
         if key is None:
             # KV-shared layer: the cache already holds every key (read with
-            # skip_kv_update); zeros only fill the operand slots.
+            # skip_kv_update); zeros only fill the operand slots, kept per
+            # shape so no call allocates them again.
             assert value is None and self.kv_sharing_target_layer_name is not None
-            key = query.new_zeros(q_len, self.num_kv_heads * self.head_size)
+            zkey = (query.device, query.dtype, q_len)
+            key = self._shared_kv_zeros.get(zkey)
+            if key is None:
+                key = query.new_zeros(q_len, self.num_kv_heads * self.head_size)
+                self._shared_kv_zeros[zkey] = key
             value = key
         k_len = key.shape[0]
         k_compute_dim = key.shape[1] * key.shape[2] if key.dim() == 3 else key.shape[1]
@@ -326,9 +332,18 @@ class RpaAttentionBackendImpl:
             key, value = quantize_kv(self.kv_cache_quantized_dtype, key, value, k_scale, v_scale)
         skip_kv_update = self.kv_sharing_target_layer_name is not None
         kernel = self._build_rpa_kernel(None, k_scale, v_scale, skip_kv_update=skip_kv_update)
+        # The kernels write [T, Hq, D] rows; when `output` has exactly that
+        # memory layout (no head padding, contiguous, the q dtype) they write
+        # into it directly instead of into a temporary that is then copied.
+        direct = (output is not None and not pad and self.head_size != 64
+                  and output.is_contiguous() and output.dtype == query.dtype
+                  and output.numel() == query.numel() and output.device == query.device)
         outputs = kernel(kv_cache, query, key, value, attn_metadata.seq_lens,
                          attn_metadata.block_tables, attn_metadata.query_start_loc,
-                         attn_metadata.request_distribution, self.sinks)
+                         attn_metadata.request_distribution, self.sinks,
+                         out=output.view(query.shape) if direct else None)
+        if direct:
+            return output
         if outputs.shape[-1] > self.head_size:
             outputs = outputs[..., :self.head_size]
         if query_dim == 2:

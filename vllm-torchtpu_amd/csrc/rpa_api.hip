@@ -179,8 +179,9 @@ int rpa_validate_desc(const rpa_desc* d) {
   if (d->decode_query_size < 0) return RPA_ERR_INVALID_ARG;
   if (d->path < RPA_PATH_AUTO || d->path > RPA_PATH_DECODE_ONLY) return RPA_ERR_INVALID_ARG;
   // Implemented combinations.
-  if (d->kv_dtype == RPA_DTYPE_F16 || d->q_dtype == RPA_DTYPE_F16) return RPA_ERR_UNSUPPORTED;
-  if (d->out_dtype != RPA_DTYPE_F32 && d->out_dtype != RPA_DTYPE_BF16) return RPA_ERR_UNSUPPORTED;
+  if (d->out_dtype != RPA_DTYPE_F32 && d->out_dtype != RPA_DTYPE_BF16 &&
+      d->out_dtype != RPA_DTYPE_F16)
+    return RPA_ERR_UNSUPPORTED;
   const bool q_is_fp8 = d->q_dtype == RPA_DTYPE_FP8_E4M3FN || d->q_dtype == RPA_DTYPE_FP8_E5M2;
   if (q_is_fp8 && d->q_dtype != d->kv_dtype) return RPA_ERR_UNSUPPORTED;
   if (d->head_dim_padded > 512) return RPA_ERR_UNSUPPORTED;

@@ -159,8 +159,12 @@ struct TE5M2 {
   }
 };
 
-// Output stores.
+// Output stores (f32; bf16 as uint16_t bits; f16 as _Float16, round to
+// nearest even).
 __device__ __forceinline__ void store_out(float* p, int64_t i, float v) { p[i] = v; }
+__device__ __forceinline__ void store_out(_Float16* p, int64_t i, float v) {
+  p[i] = static_cast<_Float16>(v);
+}
 __device__ __forceinline__ void store_out(uint16_t* p, int64_t i, float v) {
   p[i] = f32_to_bf16_bits(v);
 }

@@ -1,8 +1,8 @@
 // Shape-generic RPA attention: one wavefront per (token row, q head).
 //
 // This path covers every shape and dtype combination the library accepts
-// (any q-heads-per-kv-head ratio, any head_dim up to 512, f32/bf16/fp8 KV,
-// f32/bf16 output).  It runs after the KV-page write kernel, so every key is
+// (any q-heads-per-kv-head ratio, any head_dim up to 512, f32/bf16/f16/fp8
+// KV, f32/bf16/f16 output).  It runs after the KV-page write kernel, so every key is
 // read from the cache.  The per-row computation (generic_row) is shared with
 // the finish kernel.
 #include "rpa_common.h"
@@ -75,6 +75,8 @@ hipError_t dispatch_kv(const Params& p, int kv_dtype, const void* q, const void*
       return launch3<QT, TF32, OutS>(p, q, cache, kv_lens, page_indices, cu, dist, out, stream);
     case RPA_DTYPE_BF16:
       return launch3<QT, TBF16, OutS>(p, q, cache, kv_lens, page_indices, cu, dist, out, stream);
+    case RPA_DTYPE_F16:
+      return launch3<QT, TF16, OutS>(p, q, cache, kv_lens, page_indices, cu, dist, out, stream);
     case RPA_DTYPE_FP8_E4M3FN:
       return launch3<QT, TE4M3, OutS>(p, q, cache, kv_lens, page_indices, cu, dist, out, stream);
     case RPA_DTYPE_FP8_E5M2:
@@ -93,6 +95,8 @@ hipError_t dispatch_q(const Params& p, int q_dtype, int kv_dtype, const void* q,
       return dispatch_kv<TF32, OutS>(p, kv_dtype, q, cache, kv_lens, page_indices, cu, dist, out, stream);
     case RPA_DTYPE_BF16:
       return dispatch_kv<TBF16, OutS>(p, kv_dtype, q, cache, kv_lens, page_indices, cu, dist, out, stream);
+    case RPA_DTYPE_F16:
+      return dispatch_kv<TF16, OutS>(p, kv_dtype, q, cache, kv_lens, page_indices, cu, dist, out, stream);
     case RPA_DTYPE_FP8_E4M3FN:
       return launch3<TE4M3, TE4M3, OutS>(p, q, cache, kv_lens, page_indices, cu, dist, out, stream);
     case RPA_DTYPE_FP8_E5M2:
@@ -113,6 +117,8 @@ hipError_t launch_attn_generic(const Params& p, int q_dtype, int kv_dtype, int o
     return dispatch_q<float>(p, q_dtype, kv_dtype, q, kv_cache, kv_lens, page_indices, cu, dist, out, stream);
   if (out_dtype == RPA_DTYPE_BF16)
     return dispatch_q<uint16_t>(p, q_dtype, kv_dtype, q, kv_cache, kv_lens, page_indices, cu, dist, out, stream);
+  if (out_dtype == RPA_DTYPE_F16)
+    return dispatch_q<_Float16>(p, q_dtype, kv_dtype, q, kv_cache, kv_lens, page_indices, cu, dist, out, stream);
   return hipErrorInvalidValue;
 }
 

@@ -29,6 +29,7 @@ the design notes:
 from __future__ import annotations
 
 import enum
+import warnings
 from typing import Any
 
 import torch
@@ -45,6 +46,7 @@ __all__ = [
     "ragged_paged_attention",
     "ragged_paged_attention_bundled",
     "rpa_kv_cache_update",
+    "reserve_workspace",
     "merge_attn_results",
     "merge_attn_states",
 ]
@@ -277,14 +279,43 @@ def _require_device(*tensors: torch.Tensor) -> torch.device:
 
 # Per-device workspace (decode partials and work plan), grown on demand and
 # kept.  Calls that share a device's workspace must be ordered on one stream
-# (as vLLM's are).
+# (as vLLM's are).  A HIP graph captured over a call keeps that call's
+# workspace pointer, so a workspace is never freed once handed out: a larger
+# one replaces it for later calls and the old one stays alive in _RETIRED.
+# Growing during a capture would allocate inside it, so that raises: reserve
+# the largest workspace first (reserve_workspace, or one eager call of the
+# largest shape, as vLLM's warm-up does).
 _WORKSPACES: dict = {}
+_RETIRED: list = []
+# Largest max_num_seqs the fast kernels' in-LDS plan holds (rpa_internal.h,
+# kMaxDecodeSeqs); larger batches run on the shape-generic kernels.
+MAX_FAST_SEQS = 2048
+_WARNED_GENERIC = set()
+
+
+def _ws_key(device: torch.device):
+    if device.type == "cuda" and device.index is None:
+        return (device.type, torch.cuda.current_device())
+    return (device.type, device.index)
+
+
+def reserve_workspace(device, nbytes: int) -> torch.Tensor:
+    """Make the workspace of `device` at least `nbytes` (call before capturing
+    graphs whose calls need more than eager calls so far did)."""
+    return _workspace(torch.device(device), nbytes)
 
 
 def _workspace(device: torch.device, nbytes: int) -> torch.Tensor:
-    key = device.index if device.index is not None else torch.cuda.current_device()
+    key = _ws_key(device)
     buf = _WORKSPACES.get(key)
     if buf is None or buf.numel() < nbytes:
+        if device.type == "cuda" and torch.cuda.is_current_stream_capturing():
+            raise RuntimeError(
+                f"the RPA workspace on {device} must grow to {nbytes} bytes during graph "
+                "capture; reserve it first (vllm_torchtpu_amd.rpa.reserve_workspace, or one "
+                "eager call of the largest shape before capturing)")
+        if buf is not None:
+            _RETIRED.append(buf)
         buf = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=device)
         _WORKSPACES[key] = buf
     return buf
@@ -310,6 +341,12 @@ def _rpa_forward_impl(queries, keys, values, kv_cache, kv_lens, page_indices, cu
                       q_scale=q_scale, k_scale=k_scale, v_scale=v_scale, path=path,
                       decode_query_size=decode_query_size)
     N.check(L.rpa_validate_desc(desc), "rpa_validate_desc")
+    if desc.max_num_seqs > MAX_FAST_SEQS and desc.max_num_seqs not in _WARNED_GENERIC:
+        _WARNED_GENERIC.add(desc.max_num_seqs)
+        warnings.warn(
+            f"max_num_seqs={desc.max_num_seqs} exceeds {MAX_FAST_SEQS}, the most the decode and "
+            "prefill kernels plan for: this call runs on the shape-generic kernels (correct, "
+            "but not a fast path)", RuntimeWarning, stacklevel=3)
     with torch.cuda.device(queries.device):
         ws_bytes = int(L.rpa_workspace_size(desc))
         if workspace is None:
@@ -392,6 +429,30 @@ def _(queries, keys, values, kv_cache, kv_lens, page_indices, cu_q_lens, distrib
             torch.empty(queries.shape[:2], dtype=torch.float32, device=queries.device))
 
 
+# The same op writing into a caller-provided output (the attention backend's
+# `output` buffer): mutates kv_cache and out, returns nothing.
+@torch.library.custom_op("rpa_amd::ragged_paged_attention_out", mutates_args=("kv_cache", "out"))
+def _rpa_out_op(queries: torch.Tensor, keys: torch.Tensor, values: torch.Tensor,
+                kv_cache: torch.Tensor, kv_lens: torch.Tensor, page_indices: torch.Tensor,
+                cu_q_lens: torch.Tensor, distribution: torch.Tensor, out: torch.Tensor,
+                use_causal_mask: bool, skip_kv_update: bool, sm_scale: float,
+                sliding_window: int, soft_cap: float, has_soft_cap: bool, q_scale: float,
+                k_scale: float, v_scale: float, path: int, decode_query_size: int) -> None:
+    _rpa_forward_impl(
+        queries, keys, values, kv_cache, kv_lens, page_indices, cu_q_lens, distribution, out,
+        use_causal_mask=use_causal_mask, skip_kv_update=skip_kv_update, sm_scale=sm_scale,
+        sliding_window=sliding_window if sliding_window > 0 else None,
+        soft_cap=soft_cap if has_soft_cap else None, q_scale=q_scale, k_scale=k_scale,
+        v_scale=v_scale, path=path, decode_query_size=decode_query_size)
+
+
+@_rpa_out_op.register_fake
+def _(queries, keys, values, kv_cache, kv_lens, page_indices, cu_q_lens, distribution, out,
+      use_causal_mask, skip_kv_update, sm_scale, sliding_window, soft_cap, has_soft_cap,
+      q_scale, k_scale, v_scale, path, decode_query_size):
+    return None
+
+
 def ragged_paged_attention(
     queries: torch.Tensor,  # [max_num_tokens, actual_num_q_heads, actual_head_dim]
     keys: torch.Tensor,  # [max_num_tokens, actual_num_kv_heads, actual_head_dim]
@@ -424,6 +485,7 @@ def ragged_paged_attention(
     disable_semaphore_checks: bool = True,
     return_lse: bool = False,
     decode_query_size: int = 1,
+    out: torch.Tensor | None = None,
 ):
     """Ragged paged attention with mixed prefill and decode (kernel.py:1633-1984).
 
@@ -443,6 +505,11 @@ def ragged_paged_attention(
     (speculative-decoding verify windows of K + 1 tokens).  Sequences with up to
     that many new tokens run on the decode kernel (while q_len * Hq/Hkv <= 16);
     the result does not depend on it.
+
+    out (an addition for the attention backend, whose forward receives an
+    output buffer): a contiguous [max_num_tokens, Hq, D] tensor in the q dtype
+    on the same device; the rows are written there and `out` is returned.
+    Not combinable with return_lse.
     """
     del debug_mode, disable_bounds_checks, disable_semaphore_checks
     static_validate_inputs(
@@ -467,6 +534,22 @@ def ragged_paged_attention(
         # cast to the KV dtype; q_scale is multiplied back into the logits.
         info = torch.finfo(kv_cache.dtype)
         q = torch.clamp(q / q_scale, min=info.min, max=info.max).to(kv_cache.dtype)
+    if out is not None:
+        if return_lse:
+            raise ValueError("out= and return_lse=True cannot be combined")
+        if (out.dtype != result_dtype or tuple(out.shape) != tuple(queries.shape)
+                or not out.is_contiguous() or out.device != queries.device):
+            raise ValueError(f"out must be a contiguous {result_dtype} tensor of shape "
+                             f"{tuple(queries.shape)} on {queries.device}")
+        torch.ops.rpa_amd.ragged_paged_attention_out(
+            q.contiguous(), keys.contiguous(), values.contiguous(), kv_cache, kv_lens,
+            page_indices, cu_q_lens, distribution, out, bool(use_causal_mask),
+            bool(skip_kv_update), float(sm_scale),
+            0 if sliding_window is None else int(sliding_window),
+            0.0 if soft_cap is None else float(soft_cap), soft_cap is not None,
+            1.0 if q_scale is None else float(q_scale), 1.0 if k_scale is None else float(k_scale),
+            1.0 if v_scale is None else float(v_scale), N.RPA_PATH_AUTO, int(decode_query_size))
+        return out, kv_cache
     op = (torch.ops.rpa_amd.ragged_paged_attention_lse if return_lse
           else torch.ops.rpa_amd.ragged_paged_attention)
     res = op(
@@ -482,31 +565,36 @@ def ragged_paged_attention(
     return res, kv_cache
 
 
-def merge_attn_states(outs: torch.Tensor, lses: torch.Tensor):
+def merge_attn_states(outs: torch.Tensor, lses: torch.Tensor, out_dtype=torch.float32):
     """LSE-weighted merge of R partial attentions of the same rows.
 
     outs [R, ..., D] (bf16 or f32), lses [R, ...] (natural-log LSE, any float
-    dtype; computed in f32) -> (out [..., D] in outs.dtype, lse [...] f32).
+    dtype; computed in f32) -> (out [..., D] in out_dtype, lse [...] f32).
     merge_attn_results (cp_attention.py:45-72) generalised to R partials, on
     the GPU (rpa_merge_attn_states in include/rpa.h): weights exp(lse_r - m)
-    with m = max_r lse_r, NaN/inf partial outputs counted as 0, rows whose
-    partials all have lse -inf give 0 and lse -inf.
+    with m = max_r lse_r (a NaN lse propagates, as torch.maximum), NaN/inf
+    partial outputs counted as 0, rows whose partials all have lse -inf give
+    0 and lse -inf.  out_dtype defaults to f32, the reference's result dtype
+    (its f32 weights promote bf16 partials); bf16 is also accepted.
     """
     if outs.dim() < 2 or lses.shape != outs.shape[:-1]:
         raise ValueError(f"outs {tuple(outs.shape)} and lses {tuple(lses.shape)} do not match")
     if not outs.is_cuda or lses.device != outs.device:
         raise RuntimeError("merge_attn_states: tensors must be on one GPU (no CPU fallback)")
+    if out_dtype not in (torch.float32, torch.bfloat16):
+        raise ValueError(f"out_dtype {out_dtype} is not supported (f32 or bf16)")
     parts, dim = outs.shape[0], outs.shape[-1]
     rows = outs[0].numel() // max(dim, 1)
     outs_c = outs.contiguous()
     lses_c = lses.to(torch.float32).contiguous()
-    out = torch.empty(outs.shape[1:], dtype=outs.dtype, device=outs.device)
+    out = torch.empty(outs.shape[1:], dtype=out_dtype, device=outs.device)
     lse = torch.empty(lses.shape[1:], dtype=torch.float32, device=outs.device)
     L = N.lib()
     with torch.cuda.device(outs.device):
         stream = torch.cuda.current_stream(outs.device).cuda_stream
-        code = L.rpa_merge_attn_states(parts, rows, dim, N.rpa_dtype(outs.dtype), _ptr(outs_c),
-                                       _ptr(lses_c), _ptr(out), _ptr(lse), stream)
+        code = L.rpa_merge_attn_states(parts, rows, dim, N.rpa_dtype(outs.dtype),
+                                       N.rpa_dtype(out_dtype), _ptr(outs_c), _ptr(lses_c),
+                                       _ptr(out), _ptr(lse), stream)
     N.check(code, "rpa_merge_attn_states")
     return out, lse
 
@@ -515,7 +603,7 @@ def merge_attn_results(out_a: torch.Tensor, lse_a: torch.Tensor, out_b: torch.Te
                        lse_b: torch.Tensor):
     """Numerically stable LSE-weighted combination of two partial attentions
     (cp_attention.py:45-72): out [T, H, D], lse [T, H] (natural log) each;
-    returns (combined_out, combined_lse f32)."""
+    returns (combined_out f32, combined_lse f32), the reference's dtypes."""
     if out_a.shape != out_b.shape or lse_a.shape != lse_b.shape:
         raise ValueError("merge_attn_results: partials differ in shape")
     return merge_attn_states(torch.stack([out_a, out_b]),
