@@ -79,8 +79,11 @@ def test_validate_desc_codes():
     assert L.rpa_validate_desc(_desc(head_dim_padded=256)) == N.RPA_ERR_INVALID_ARG
     assert L.rpa_validate_desc(_desc(kv_heads_x2=6)) == N.RPA_ERR_INVALID_ARG
     assert L.rpa_validate_desc(_desc(has_soft_cap=1, soft_cap=0.0)) == N.RPA_ERR_INVALID_ARG
-    assert L.rpa_validate_desc(_desc(kv_dtype=N.RPA_DTYPE_F16, q_dtype=N.RPA_DTYPE_F16)) in (
-        N.RPA_ERR_INVALID_ARG, N.RPA_ERR_UNSUPPORTED)
+    # f16 q and KV (any float KV dtype, kernel.py:1447-1453) run on the generic kernels.
+    assert L.rpa_validate_desc(_desc(kv_dtype=N.RPA_DTYPE_F16, q_dtype=N.RPA_DTYPE_F16,
+                                     out_dtype=N.RPA_DTYPE_F16)) == N.RPA_OK
+    assert L.rpa_validate_desc(_desc(out_dtype=99)) in (N.RPA_ERR_INVALID_ARG,
+                                                        N.RPA_ERR_UNSUPPORTED)
     assert L.rpa_validate_desc(_desc(decode_query_size=-1)) == N.RPA_ERR_INVALID_ARG
     assert L.rpa_workspace_size(_desc()) > 0
     assert L.rpa_workspace_size(_desc(abi_version=99)) == 0
