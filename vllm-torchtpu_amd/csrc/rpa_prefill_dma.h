@@ -37,21 +37,25 @@
 // helpers it shares with prefill_kernel.)
 #pragma once
 
+template <int DP_>
 struct DmaCfg {
-  static constexpr int DP = 128;
-  static constexpr int THREADS = 512;
+  static constexpr int DP = DP_;
+  // head_dim 128: 8 wavefronts, two per SIMD (256 registers each); head_dim
+  // 256: 4 wavefronts, one per SIMD (the O and Q operands alone take 192).
+  static constexpr int THREADS = DP <= 128 ? 512 : 256;
   static constexpr int WAVES = THREADS / 64;
-  static constexpr int ROWS = 256;                 // q rows per item (32 per wavefront)
-  static constexpr int BK = 64;                    // keys per tile
-  static constexpr int NSB = BK / 32;              // 32-key sub-blocks per tile
+  static constexpr int ROWS = 32 * WAVES;          // q rows per item (32 per wavefront)
   static constexpr int ROWB = 2 * DP;              // bytes of one key's K (or V) row
+  static constexpr int BK = 16384 / ROWB;          // keys per tile: 16 KiB of K, 16 KiB of V
+  static constexpr int NSB = BK / 32;              // 32-key sub-blocks per tile
   static constexpr int TILE = BK * ROWB;           // 16 KiB
   static constexpr int CHUNKS = TILE / 1024;       // 1-KiB copies per K (or V) tile
   static constexpr int CPW = CHUNKS / WAVES;       // per wavefront
+  static constexpr int CPR = ROWB / 16;            // 16-byte chunks per row
   static constexpr int KSTEPS = DP / 16;           // QK^T k-steps
   static constexpr int NT = DP / 32;               // 32-dim output blocks
   static constexpr int PLAN_BYTES = static_cast<int>(sizeof(PlanCore) + sizeof(PlanRows));
-  static_assert(CHUNKS % WAVES == 0, "whole copies per wavefront");
+  static_assert(CHUNKS % WAVES == 0 && NSB >= 1, "whole copies per wavefront");
   static_assert(PLAN_BYTES >= 4 * (kMaxDecodeSeqs + 1), "block prefix fits the plan scratch");
 };
 
@@ -149,8 +153,9 @@ __device__ __forceinline__ int32_t longest_first_block(const Params& p, const in
 
 // CAP: the logit soft cap is on (a template parameter, so the score
 // transform has no per-element branches).
-template <typename OutS, bool CAP>
-__global__ void __launch_bounds__(DmaCfg::THREADS) __attribute__((amdgpu_waves_per_eu(2)))
+template <int DP_, typename OutS, bool CAP>
+__global__ void __launch_bounds__(DmaCfg<DP_>::THREADS)
+__attribute__((amdgpu_waves_per_eu(DP_ <= 128 ? 2 : 1)))
 prefill_dma_kernel(Params p, const uint16_t* __restrict__ q, const uint16_t* __restrict__ keys,
                    const uint16_t* __restrict__ values, uint16_t* __restrict__ cache,
                    const int32_t* __restrict__ kv_lens, const int32_t* __restrict__ page_indices,
@@ -158,7 +163,7 @@ prefill_dma_kernel(Params p, const uint16_t* __restrict__ q, const uint16_t* __r
                    OutS* __restrict__ out, const int32_t* __restrict__ plan,
                    const float* __restrict__ part_o, const float* __restrict__ part_ml,
                    int32_t nfm, int32_t nfw) {
-  using C = DmaCfg;
+  using C = DmaCfg<DP_>;
   constexpr int DP = C::DP, BK = C::BK;
   // Separate arrays per buffer: reads of one are never ordered after copies
   // into another.
@@ -180,13 +185,16 @@ prefill_dma_kernel(Params p, const uint16_t* __restrict__ q, const uint16_t* __r
   // ---- finish workgroups: [0, nfm) merge items, the last nfw write items.
   const int32_t blk_id = static_cast<int32_t>(blockIdx.x);
   const int32_t nattn = static_cast<int32_t>(gridDim.x) - nfm - nfw;
-  if (blk_id < nfm || blk_id >= nfm + nattn) {
-    const bool merges = blk_id < nfm;
-    prefill_finish_role<uint16_t, DP, OutS>(p, aux, keys, values, cache, kv_lens, page_indices,
-                                            cu, dist, out, plan, part_o, part_ml, merges,
-                                            merges ? nfm : nfw,
-                                            merges ? blk_id : blk_id - nfm - nattn, C::WAVES);
-    return;
+  // At head_dim 256 the finish kernel does this work (nfm = nfw = 0).
+  if constexpr (kPrefillFinishRoles<DP>) {
+    if (blk_id < nfm || blk_id >= nfm + nattn) {
+      const bool merges = blk_id < nfm;
+      prefill_finish_role<uint16_t, DP, OutS>(p, aux, keys, values, cache, kv_lens,
+                                              page_indices, cu, dist, out, plan, part_o, part_ml,
+                                              merges, merges ? nfm : nfw,
+                                              merges ? blk_id : blk_id - nfm - nattn, C::WAVES);
+      return;
+    }
   }
   const int32_t bid = blk_id - nfm;
   if (decode_on && plan[3] == 0) return;
@@ -286,8 +294,8 @@ prefill_dma_kernel(Params p, const uint16_t* __restrict__ q, const uint16_t* __r
 #pragma unroll
     for (int i = 0; i < C::CPW; ++i) {
       const int c = wave + C::WAVES * i;
-      const int key = 4 * c + (lane >> 4);
-      const int j = lane & 15;
+      const int key = (1024 / C::ROWB) * c + lane / C::CPR;
+      const int j = lane % C::CPR;
       const unsigned char* ka = reinterpret_cast<const unsigned char*>(ktab[slot][key][0]);
       const unsigned char* va = reinterpret_cast<const unsigned char*>(ktab[slot][key][1]);
       const uint32_t kl = __builtin_amdgcn_readfirstlane(kbuf + 1024 * c);
@@ -307,13 +315,14 @@ prefill_dma_kernel(Params p, const uint16_t* __restrict__ q, const uint16_t* __r
       qop[kk] = *reinterpret_cast<const uint4*>(qrow + 16 * kk + 8 * half);
   }
 
-  // Swizzled operand offsets.  K: key 32 sb + col, chunk 2 kk + half at
-  // chunk (2 kk + half) ^ (col & 15): byte (kbase ^ 32 kk) + 8192 sb.
+  // Swizzled operand offsets (ROWB-byte rows).  K: key 32 sb + col, chunk
+  // 2 kk + half at chunk (2 kk + half) ^ (col & 15): byte (kbase ^ 32 kk) +
+  // 32 ROWB sb.
   const uint32_t kbase = col * C::ROWB + 16 * (half ^ (col & 15));
   // V (ds_read_b64_tr_b16, 16-lane group G, lane jl): key 32 sb + 16 ks +
   // 4 (G >> 1) + jl / 4 (+ 8 for the second read), dims 32 tt + 16 (G & 1) +
   // 4 (jl & 3): chunk 4 tt + 2 (G & 1) + ((jl >> 1) & 1) at chunk ^ 4 (jl >> 2),
-  // byte (vbase ^ 64 tt) + 8192 sb + 4096 ks (+ 2048).
+  // byte (vbase ^ 64 tt) + 32 ROWB sb + 16 ROWB ks (+ 8 ROWB).
   const int G = lane >> 4, jl = lane & 15;
   const uint32_t vbase = (4 * (G >> 1) + (jl >> 2)) * C::ROWB + 64 * (jl >> 2) +
                          16 * (2 * (G & 1) + ((jl >> 1) & 1)) + 8 * (jl & 1);
@@ -334,7 +343,7 @@ prefill_dma_kernel(Params p, const uint16_t* __restrict__ q, const uint16_t* __r
     for (int sb = 0; sb < C::NSB; ++sb) {
       constexpr int kRA = 4;  // K operand reads in flight
       auto kread = [&](int kk) __attribute__((always_inline)) -> uint4 {
-        return *reinterpret_cast<const uint4*>(kbuf + 8192 * sb + (kbase ^ (32u * kk)));
+        return *reinterpret_cast<const uint4*>(kbuf + 32 * C::ROWB * sb + (kbase ^ (32u * kk)));
       };
       f32x16_t sacc = f32x16_t{};
       uint4 kb[kRA];
@@ -406,7 +415,8 @@ prefill_dma_kernel(Params p, const uint16_t* __restrict__ q, const uint16_t* __r
       constexpr int kP = 2 * C::NT;
       auto vread = [&](int i) __attribute__((always_inline)) -> uint4 {
         const int ks = i / C::NT, tt = i % C::NT;
-        const unsigned char* ra = vbuf + 8192 * sb + 4096 * ks + (vbase ^ (64u * tt));
+        const unsigned char* ra =
+            vbuf + 32 * C::ROWB * sb + 16 * C::ROWB * ks + (vbase ^ (64u * tt));
         const v4i16 va = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
             (__attribute__((address_space(3))) v4i16*)ra);
         const v4i16 vb = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
