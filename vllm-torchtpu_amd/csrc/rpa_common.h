@@ -210,12 +210,29 @@ __device__ __forceinline__ void wave_lds_sync() {
 
 // logit transform shared by every attention kernel: scale then soft cap
 // (kernel.py:185-194): s = cap * tanh(s / cap).  tanh is built from exp:
-// tanh(x) = 1 - 2 / (exp(2x) + 1), exact at the limits (+-1) and odd.
+// tanh(x) = 1 - 2 / (exp(2x) + 1), exact at the limits (+-1) and odd.  The
+// exponential is v_exp_f32 (2^y with y = 2 x log2 e) and the reciprocal
+// v_rcp_f32 (1 ulp each), not an IEEE division: the result is within a few
+// ulp of cap (absolute), far inside every tolerance the logits feed.
 __device__ __forceinline__ float soft_cap_fn(float s, float cap, float inv_cap) {
-  const float x = s * inv_cap;
-  const float e = __expf(2.0f * x);
-  const float t = 1.0f - 2.0f / (e + 1.0f);
-  return cap * t;
+  const float e = __builtin_amdgcn_exp2f(s * (inv_cap * 2.8853900817779268f));  // e^(2 s / cap)
+  const float r = __builtin_amdgcn_rcpf(e + 1.0f);
+  return cap * fmaf(-2.0f, r, 1.0f);
+}
+
+// The same transform of a raw dot product x, in log2 units, with the
+// constants folded: a = sm-scale * 2 log2(e) / cap, b = cap * log2(e);
+// returns b * tanh(x * sm-scale / cap) = b - 2 b / (2^(a x) + 1).
+__device__ __forceinline__ float soft_cap_log2(float x, float a, float b) {
+  const float r = __builtin_amdgcn_rcpf(__builtin_amdgcn_exp2f(x * a) + 1.0f);
+  return fmaf(-2.0f * b, r, b);
+}
+struct SoftCapLog2 {
+  float a, b;
+};
+__device__ __forceinline__ SoftCapLog2 soft_cap_log2_consts(const Params& p) {
+  return SoftCapLog2{p.score_scale * p.inv_cap * 2.8853900817779268f,
+                     p.cap * 1.4426950408889634f};
 }
 
 }  // namespace rpa

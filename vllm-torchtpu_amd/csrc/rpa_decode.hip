@@ -382,6 +382,7 @@ decode_kernel(Params p, const uint16_t* __restrict__ q, const typename KV::stora
   TileInfo nxt = advance(cur);
   pages_of(nxt.g < g_end ? nxt : cur, pbuf[0]);
 
+  const SoftCapLog2 capk = soft_cap_log2_consts(p);
   float m_run = -INFINITY;  // per row n, in log2 units
   float l_run = 0.0f;       // this lane's share of the row sum
   f32x4_t oacc[NT];
@@ -471,7 +472,7 @@ decode_kernel(Params p, const uint16_t* __restrict__ q, const typename KV::stora
     if (p.has_cap) {
 #pragma unroll
       for (int i = 0; i < 4 * NG; ++i)
-        sc[i] = soft_cap_fn(sc[i] * p.score_scale, p.cap, p.inv_cap) * kLog2e;
+        sc[i] = soft_cap_log2(sc[i], capk.a, capk.b);
     } else {
 #pragma unroll
       for (int i = 0; i < 4 * NG; ++i) sc[i] *= p.score_scale * kLog2e;

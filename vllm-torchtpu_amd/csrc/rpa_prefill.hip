@@ -365,6 +365,7 @@ prefill_kernel(Params p, const uint16_t* __restrict__ q,
   };
 
   const float cm = p.has_cap ? 1.0f : p.score_scale * kLog2e;  // multiplier into log2 units
+  const SoftCapLog2 capk = soft_cap_log2_consts(p);
   f32x16_t oacc[C::NT];
 #pragma unroll
   for (int t = 0; t < C::NT; ++t) oacc[t] = f32x16_t{};
@@ -441,7 +442,7 @@ prefill_kernel(Params p, const uint16_t* __restrict__ q,
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
           float x = sacc[i];
-          if (p.has_cap) x = soft_cap_fn(x * p.score_scale, p.cap, p.inv_cap) * kLog2e;
+          if (p.has_cap) x = soft_cap_log2(x, capk.a, capk.b);
           y[i] = x;
         }
         // A non-positive multiplier is applied before masking (the max and

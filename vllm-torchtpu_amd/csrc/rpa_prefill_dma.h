@@ -328,6 +328,7 @@ prefill_dma_kernel(Params p, const uint16_t* __restrict__ q, const uint16_t* __r
                          16 * (2 * (G & 1) + ((jl >> 1) & 1)) + 8 * (jl & 1);
 
   const float cm = CAP ? 1.0f : p.score_scale * kLog2e;
+  const SoftCapLog2 capk = soft_cap_log2_consts(p);
   f32x16_t oacc[C::NT];
 #pragma unroll
   for (int t = 0; t < C::NT; ++t) oacc[t] = f32x16_t{};
@@ -369,7 +370,7 @@ prefill_dma_kernel(Params p, const uint16_t* __restrict__ q, const uint16_t* __r
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
         float x = sacc[i];
-        if constexpr (CAP) x = soft_cap_fn(x * p.score_scale, p.cap, p.inv_cap) * kLog2e;
+        if constexpr (CAP) x = soft_cap_log2(x, capk.a, capk.b);
         y[i] = x;
       }
       float cme = cm;
