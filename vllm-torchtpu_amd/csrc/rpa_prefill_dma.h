@@ -1,24 +1,27 @@
-// Prefill attention for bf16 KV at head_dim 128: key tiles copied straight
-// from HBM into LDS (gfx950's global_load_lds_dwordx4), no register staging.
+// Prefill attention for bf16 KV at head_dim 128 and 256 (unpadded): key
+// tiles copied straight from HBM into LDS (gfx950's global_load_lds_dwordx4),
+// no register staging.
 //
-// Included by rpa_prefill.hip, whose prefill_kernel it replaces for this
-// shape.  The item decomposition, row layout and math are the same: a
-// workgroup of 8 wavefronts owns 256 q rows (BQ = 256 / qpk query tokens of
-// one sequence times the qpk q heads of one kv head), wavefront w owns rows
+// Included by rpa_prefill.hip, whose prefill_kernel it replaces for these
+// shapes.  The item decomposition, row layout and math are the same: a
+// workgroup of 8 wavefronts (4 at head_dim 256) owns 256 (128) q rows
+// (BQ = rows / qpk query tokens of one sequence times the qpk q heads of one
+// kv head), wavefront w owns rows
 // [32w, 32w + 32), lane l owns MFMA column l % 32, and per 32-key sub-block
 //   S^T[key, row] = K[key, :] . Q^T[:, row]          (v_mfma_f32_32x32x16_bf16)
 //   O^T[dim, row] += V^T[dim, key] . P^T[key, row]    (V^T via ds_read_b64_tr_b16)
 // with an online softmax in the column layout.
 //
 // What changes is the tile path:
-//   * Three LDS tile buffers (64 keys: 16 KiB of K, 16 KiB of V each), filled
-//     by LDS-DMA: each wavefront issues four 1-KiB copies per tile (64 lanes x
+//   * Three LDS tile buffers (16 KiB of K and 16 KiB of V each: 64 keys at
+//     head_dim 128, 32 at 256), filled by LDS-DMA: each wavefront issues
+//     16 / WAVES 1-KiB copies per K (and per V) tile (64 lanes x
 //     16 bytes land contiguously), so no VGPRs hold tiles in flight and no
 //     ds_write is issued.  A wavefront issues its copies of tile t + 2 after
 //     computing tile t (issued before the compute, as the measured variants
 //     with three or four buffers did, they slowed it: C3 prefill 443-452 us
 //     against 430 us).
-//   * Rows are stored unpadded (256 bytes) with an XOR swizzle of their
+//   * Rows are stored unpadded (2 x head_dim bytes) with an XOR swizzle of their
 //     16-byte chunks, chosen per operand read pattern:
 //       K: chunk c of key k sits at chunk c ^ (k & 15): the 16 lanes that read
 //          chunk c of 16 consecutive keys hit 16 distinct chunks (all 64 banks).
