@@ -77,6 +77,11 @@ __device__ __forceinline__ float bf16_bits_to_f32(uint16_t b) {
 }
 
 // Round-to-nearest-even f32 -> bf16 bits; NaN stays a quiet NaN.
+// Lazy rescaling of the online softmax: a row's reference max moves only when
+// a tile's max exceeds it by more than 2^kRescaleLog2 (P values then stay
+// below 2^8), so most tiles skip the rescale of the accumulators.
+constexpr float kRescaleLog2 = 8.0f;
+
 __device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
   uint32_t u = __float_as_uint(f);
   if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<uint16_t>((u >> 16) | 0x40u);

@@ -89,9 +89,11 @@ struct KvFP8 {
 
 __device__ __forceinline__ bf16x8_t as_bf16x8(uint4 v) { return __builtin_bit_cast(bf16x8_t, v); }
 
+// Two floats -> packed bf16 pair, round to nearest even (v_cvt_pk_bf16_f32).
 __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
-  return static_cast<uint32_t>(f32_to_bf16_bits(lo)) |
-         (static_cast<uint32_t>(f32_to_bf16_bits(hi)) << 16);
+  typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+  typedef float f32x2_t __attribute__((ext_vector_type(2)));
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{lo, hi}, bf16x2_t));
 }
 
 
@@ -477,30 +479,42 @@ decode_kernel(Params p, const uint16_t* __restrict__ q, const typename KV::stora
 #pragma unroll
       for (int i = 0; i < 4 * NG; ++i) sc[i] *= p.score_scale * kLog2e;
     }
+    // Masks: one-token groups only on a pair's last tile (keys past kv_len);
+    // multi-token groups per column (causal position and window).
+    if (MULTI || base + TT > cur.hi) {
+#pragma unroll
+      for (int i = 0; i < 4 * NG; ++i) {
+        const int32_t j = base + 16 * (i >> 2) + 4 * g + (i & 3);
+        if constexpr (MULTI)
+          sc[i] = (j <= pos && j >= klo) ? sc[i] : -INFINITY;
+        else
+          sc[i] = (j < cur.hi) ? sc[i] : -INFINITY;
+      }
+    }
     float tmax = -INFINITY;
 #pragma unroll
-    for (int i = 0; i < 4 * NG; ++i) {
-      const int32_t j = base + 16 * (i >> 2) + 4 * g + (i & 3);
-      if constexpr (MULTI)
-        sc[i] = (j <= pos && j >= klo) ? sc[i] : -INFINITY;
-      else
-        sc[i] = (j < cur.hi) ? sc[i] : -INFINITY;
-      tmax = fmaxf(tmax, sc[i]);
-    }
+    for (int i = 0; i < 4 * NG; ++i) tmax = fmaxf(tmax, sc[i]);
     tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
     tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
-    const float m_new = fmaxf(m_run, tmax);
-    const float alpha = (m_run == -INFINITY) ? 0.0f : exp2f(m_run - m_new);
+    // The reference max m_run moves only when some column's max grew by more
+    // than 2^kRescaleLog2 (a masked column's -inf never moves it).
+    if (__any(tmax > m_run + kRescaleLog2)) {
+      const float m_new = fmaxf(m_run, tmax);
+      const float alpha =
+          (m_run == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(m_run - m_new);
+      l_run *= alpha;
+#pragma unroll
+      for (int t = 0; t < NT; ++t) oacc[t] *= alpha;
+      m_run = m_new;
+    }
+    const float m_use = (m_run == -INFINITY) ? 0.0f : m_run;
     float psum = 0.0f;
 #pragma unroll
     for (int i = 0; i < 4 * NG; ++i) {
-      sc[i] = (sc[i] == -INFINITY) ? 0.0f : exp2f(sc[i] - m_new);
+      sc[i] = __builtin_amdgcn_exp2f(sc[i] - m_use);  // -inf -> 0
       psum += sc[i];
     }
-    l_run = l_run * alpha + psum;
-    m_run = m_new;
-#pragma unroll
-    for (int t = 0; t < NT; ++t) oacc[t] *= alpha;
+    l_run += psum;
 
     // ---- V: registers -> LDS rows (stride VS) -> V^T operand via
     // ds_read_b64_tr_b16.  In 16-lane group g, source lane j points at token

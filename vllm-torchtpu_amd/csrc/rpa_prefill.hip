@@ -123,9 +123,6 @@ struct PrefillCfg {
 // Page ids of an item's key range kept in LDS (longer ranges read the page
 // table directly).
 constexpr int kItemPages = 512;
-// Lazy rescaling: a row's reference max moves only when a tile's max exceeds
-// it by more than 2^kRescaleLog2 (P values then stay below 2^8).
-constexpr float kRescaleLog2 = 8.0f;
 
 // Which sequences this kernel owns: every sequence with rows, except the
 // decode sequences when the decode kernel runs.
