@@ -334,28 +334,60 @@ decode_kernel(Params p, const uint16_t* __restrict__ q, const typename KV::stora
   struct Pages {
     int32_t pg[NOCT];
   };
+  // Aligned tiles (power-of-two page size >= 8, tile start a multiple of
+  // min(page size, TT)): each 8-token octet lies in one page, so its page id
+  // and record address are wavefront-uniform (scalar loads and arithmetic;
+  // the tile loads take a uniform base plus a per-lane 32-bit offset).  Lanes
+  // past the key range then read other slots of an allocated page (page
+  // index and page id clamped into the table and the cache), whose scores
+  // the last tile's mask and zeroed V rows discard.  Other tiles use per-lane
+  // tokens clamped into the range.
+  auto aligned_tile = [&](int32_t base) __attribute__((always_inline)) -> bool {
+    return p.ps_shift >= 3 && (base & (min(p.ps, TT) - 1)) == 0;
+  };
+  const int32_t lane_off = tl * static_cast<int32_t>(p.rec * C::EB) + 16 * ol;
   auto pages_of = [&](const TileInfo& ti, Pages& pp) __attribute__((always_inline)) {
     const int32_t sq = min(max(ti.s, 0), p.S - 1);
     const int32_t* ptab = page_indices + static_cast<int64_t>(sq) * p.pps;
     const int32_t base = ti.lo + ti.lt * TT;
+    if (aligned_tile(base)) {
 #pragma unroll
-    for (int o = 0; o < NOCT; ++o) pp.pg[o] = ptab[page_of(p, clamp_tok(ti, base + 8 * o + tl))];
+      for (int o = 0; o < NOCT; ++o)
+        pp.pg[o] = ptab[min((base + 8 * o) >> p.ps_shift, p.pps - 1)];
+    } else {
+#pragma unroll
+      for (int o = 0; o < NOCT; ++o)
+        pp.pg[o] = ptab[page_of(p, clamp_tok(ti, base + 8 * o + tl))];
+    }
   };
   // Tile loads: octet o, part pt -> bytes [128pt + 16ol, +16) of the head's
   // K|V chunk of that token.
   auto load_tile = [&](const TileInfo& ti, const Pages& pp, uint4 (*rb)[NPART])
                        __attribute__((always_inline)) {
     const int32_t base = ti.lo + ti.lt * TT;
+    if (aligned_tile(base)) {
 #pragma unroll
-    for (int o = 0; o < NOCT; ++o) {
-      const int32_t c = clamp_tok(ti, base + 8 * o + tl);
-      const int32_t pg = min(max(pp.pg[o], 0), p.P - 1);
-      const unsigned char* rec = reinterpret_cast<const unsigned char*>(
-          cache + (static_cast<int64_t>(pg) * p.ps + slot_of(p, c)) * p.rec +
-          static_cast<int64_t>(2 * ti.h) * DP);
+      for (int o = 0; o < NOCT; ++o) {
+        const int32_t pg = min(max(uni(pp.pg[o]), 0), p.P - 1);
+        const unsigned char* rec = reinterpret_cast<const unsigned char*>(
+            cache + (static_cast<int64_t>(pg) * p.ps + ((base + 8 * o) & (p.ps - 1))) * p.rec +
+            static_cast<int64_t>(2 * ti.h) * DP);
 #pragma unroll
-      for (int pt = 0; pt < NPART; ++pt)
-        rb[o][pt] = *reinterpret_cast<const uint4*>(rec + 128 * pt + 16 * ol);
+        for (int pt = 0; pt < NPART; ++pt)
+          rb[o][pt] = *reinterpret_cast<const uint4*>(rec + lane_off + 128 * pt);
+      }
+    } else {
+#pragma unroll
+      for (int o = 0; o < NOCT; ++o) {
+        const int32_t c = clamp_tok(ti, base + 8 * o + tl);
+        const int32_t pg = min(max(pp.pg[o], 0), p.P - 1);
+        const unsigned char* rec = reinterpret_cast<const unsigned char*>(
+            cache + (static_cast<int64_t>(pg) * p.ps + slot_of(p, c)) * p.rec +
+            static_cast<int64_t>(2 * ti.h) * DP);
+#pragma unroll
+        for (int pt = 0; pt < NPART; ++pt)
+          rb[o][pt] = *reinterpret_cast<const uint4*>(rec + 128 * pt + 16 * ol);
+      }
     }
   };
   // Q^T operand of (s, h): row n -> q head h*qpk + (n % qpk); dims 8g + 32kk
