@@ -174,6 +174,29 @@ def test_soft_cap(gpu_device, cap):
     check(w, gpu_device)
 
 
+@pytest.mark.parametrize("cap,qmul", [(50.0, 8.0), (50.0, 0.05), (60.0, 30.0), (80.0, 8.0)])
+def test_soft_cap_d256_logit_range(gpu_device, cap, qmul):
+    """head_dim 256 prefill rows whose capped logits spread over (-cap, cap):
+    the kernel fixes each row's reference max at its first tile when the cap
+    bounds the logits (cap <= 60) and rescales otherwise (cap 80).  Rows see
+    up to ~2000 keys whose magnitude grows with position, so their maxima move
+    far from the first tile's; tiny q (qmul 0.05) keeps every logit near 0."""
+    g = torch.Generator().manual_seed(4321)
+    seqs = [(96, 2000), (33, 700), (128, 128), (1, 1500)]
+    w = W.make_workload(seqs, 8, 4, 256, 16, seed=int(torch.randint(0, 1000, (1,), generator=g)),
+                        soft_cap=cap, distribution=[0, 0, len(seqs)], name="cap256")
+    w.q.mul_(qmul)
+    # Keys of later pages are larger (x1 .. x4), so a row's max keeps growing
+    # past its first tile's.  K is the even combined head: [..., head, 0, :].
+    pps = w.page_indices.shape[0] // w.kv_lens.shape[0]
+    for s in range(len(seqs)):
+        npg = (int(w.kv_lens[s]) + 15) // 16
+        for j in range(npg):
+            pg = int(w.page_indices[s * pps + j])
+            w.kv_cache[pg, :, :, 0, :] *= 1.0 + 3.0 * j / max(npg - 1, 1)
+    check(w, gpu_device)
+
+
 @pytest.mark.parametrize("dt", [E4M3, E5M2])
 @pytest.mark.parametrize("scales", [(0.5, 0.5), (None, None), (1.7, 0.6)])
 def test_fp8_kv(gpu_device, dt, scales):

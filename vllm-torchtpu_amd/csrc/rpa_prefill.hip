@@ -632,17 +632,20 @@ hipError_t launch_dp(const Params& p, const void* q, const void* k, const void* 
   if constexpr (sizeof(E) == 2) {
     // bf16 KV at head_dim 128 and 256: the LDS-DMA kernel (rpa_prefill_dma.h).
     if ((p.Dp == 128 || p.Dp == 256) && full) {
-#define RPA_DMA_LAUNCH(DPV, CAP)                                                                 \
-  hipLaunchKernelGGL((prefill_dma_kernel<DPV, OutS, CAP>), g, dim3(DmaCfg<DPV>::THREADS), 0,     \
+#define RPA_DMA_LAUNCH(DPV, CAP, FIX)                                                            \
+  hipLaunchKernelGGL((prefill_dma_kernel<DPV, OutS, CAP, FIX>), g, dim3(DmaCfg<DPV>::THREADS), 0,\
                      stream, p,                                                                  \
                      static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k),          \
                      static_cast<const uint16_t*>(v), static_cast<uint16_t*>(cache), kv_lens,   \
                      page_indices, cu, dist, static_cast<OutS*>(out), ws.plan, ws.part_o,       \
                      ws.part_ml, nfm, nfw)
       if (p.Dp == 128) {
-        if (p.has_cap) RPA_DMA_LAUNCH(128, true); else RPA_DMA_LAUNCH(128, false);
+        if (p.has_cap) RPA_DMA_LAUNCH(128, true, false); else RPA_DMA_LAUNCH(128, false, false);
       } else {
-        if (p.has_cap) RPA_DMA_LAUNCH(256, true); else RPA_DMA_LAUNCH(256, false);
+        // Soft-capped logits are bounded: a fixed reference max (no rescale).
+        if (p.has_cap && p.cap * kLog2e <= kFixRefMaxLog2) RPA_DMA_LAUNCH(256, true, true);
+        else if (p.has_cap) RPA_DMA_LAUNCH(256, true, false);
+        else RPA_DMA_LAUNCH(256, false, false);
       }
 #undef RPA_DMA_LAUNCH
       return hipGetLastError();

@@ -40,6 +40,10 @@
 // helpers it shares with prefill_kernel.)
 #pragma once
 
+// Largest soft cap (in log2 units of the logits) for which the fixed
+// reference max keeps every P in the normal range (see FIXREF below).
+constexpr float kFixRefMaxLog2 = 87.0f;
+
 template <int DP_>
 struct DmaCfg {
   static constexpr int DP = DP_;
@@ -156,7 +160,14 @@ __device__ __forceinline__ int32_t longest_first_block(const Params& p, const in
 
 // CAP: the logit soft cap is on (a template parameter, so the score
 // transform has no per-element branches).
-template <int DP_, typename OutS, bool CAP>
+// FIXREF (soft-capped logits, |y| <= b = cap * log2 e <= kFixRefMaxLog2): each
+// row's reference max is fixed at its first attended tile, m = max(tile max,
+// b - 64), and never moves, so P = 2^(y - m) stays within [2^(64 - 2b), 2^64]
+// (normal in bf16 and fp32, no overflow of P, l or O) and the accumulators are
+// never rescaled.  At head_dim 256 that keeps the compiler from moving the
+// 128 accumulator registers between AGPRs and VGPRs on every tile (the rescale
+// is a VALU use of them); results equal the rescaling kernel's up to rounding.
+template <int DP_, typename OutS, bool CAP, bool FIXREF = false>
 __global__ void __launch_bounds__(DmaCfg<DP_>::THREADS)
 __attribute__((amdgpu_waves_per_eu(DP_ <= 128 ? 2 : 1)))
 prefill_dma_kernel(Params p, const uint16_t* __restrict__ q, const uint16_t* __restrict__ keys,
@@ -394,7 +405,10 @@ prefill_dma_kernel(Params p, const uint16_t* __restrict__ q, const uint16_t* __r
       for (int i = 0; i < 16; ++i) tmax = __builtin_fmaxf(tmax, y[i]);
       tmax = xmax32(tmax);
       const float m_tile = tmax * cme;
-      if (__any(m_tile > m_ref + kRescaleLog2)) {
+      if constexpr (FIXREF) {
+        if (m_ref == -INFINITY && m_tile != -INFINITY)
+          m_ref = __builtin_fmaxf(m_tile, capk.b - 64.0f);
+      } else if (__any(m_tile > m_ref + kRescaleLog2)) {
         const float m_new = __builtin_fmaxf(m_ref, m_tile);
         const float alpha = (m_ref == -INFINITY) ? 0.0f : exp2f(m_ref - m_new);
         l_run *= alpha;
