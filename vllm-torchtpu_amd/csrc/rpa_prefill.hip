@@ -37,6 +37,8 @@
 // the Pallas kernel does (kernel.py:634-641); the finish kernel, launched
 // after this one, writes them into their pages.  P is rounded to bf16 for
 // the PV product (kernel.py:553); everything else accumulates in fp32.
+#include <type_traits>
+
 #include "rpa_common.h"
 #include "rpa_finish_items.h"
 #include "rpa_internal.h"
@@ -48,6 +50,7 @@ namespace {
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
 typedef short v4i16 __attribute__((ext_vector_type(4)));
 
 constexpr float kLog2e = 1.4426950408889634f;
@@ -632,6 +635,13 @@ hipError_t launch_dp(const Params& p, const void* q, const void* k, const void* 
   if constexpr (sizeof(E) == 2) {
     // bf16 KV at head_dim 128 and 256: the LDS-DMA kernel (rpa_prefill_dma.h).
     if ((p.Dp == 128 || p.Dp == 256) && full) {
+#define RPA_DMA_LAUNCH16(DPV, CAP, FIX)                                                          \
+  hipLaunchKernelGGL((prefill_dma_kernel<DPV, OutS, CAP, FIX, 16>), g,                           \
+                     dim3(DmaCfg<DPV, 16>::THREADS), 0, stream, p,                               \
+                     static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k),          \
+                     static_cast<const uint16_t*>(v), static_cast<uint16_t*>(cache), kv_lens,   \
+                     page_indices, cu, dist, static_cast<OutS*>(out), ws.plan, ws.part_o,       \
+                     ws.part_ml, nfm, nfw)
 #define RPA_DMA_LAUNCH(DPV, CAP, FIX)                                                            \
   hipLaunchKernelGGL((prefill_dma_kernel<DPV, OutS, CAP, FIX>), g, dim3(DmaCfg<DPV>::THREADS), 0,\
                      stream, p,                                                                  \
@@ -643,11 +653,12 @@ hipError_t launch_dp(const Params& p, const void* q, const void* k, const void* 
         if (p.has_cap) RPA_DMA_LAUNCH(128, true, false); else RPA_DMA_LAUNCH(128, false, false);
       } else {
         // Soft-capped logits are bounded: a fixed reference max (no rescale).
-        if (p.has_cap && p.cap * kLog2e <= kFixRefMaxLog2) RPA_DMA_LAUNCH(256, true, true);
-        else if (p.has_cap) RPA_DMA_LAUNCH(256, true, false);
-        else RPA_DMA_LAUNCH(256, false, false);
+        if (p.has_cap && p.cap * kLog2e <= kFixRefMaxLog2) RPA_DMA_LAUNCH16(256, true, true);
+        else if (p.has_cap) RPA_DMA_LAUNCH16(256, true, false);
+        else RPA_DMA_LAUNCH16(256, false, false);
       }
 #undef RPA_DMA_LAUNCH
+#undef RPA_DMA_LAUNCH16
       return hipGetLastError();
     }
   }

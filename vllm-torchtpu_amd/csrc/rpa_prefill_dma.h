@@ -44,14 +44,18 @@
 // reference max keeps every P in the normal range (see FIXREF below).
 constexpr float kFixRefMaxLog2 = 87.0f;
 
-template <int DP_>
+template <int DP_, int RW_ = 32>
 struct DmaCfg {
   static constexpr int DP = DP_;
-  // head_dim 128: 8 wavefronts, two per SIMD (256 registers each); head_dim
-  // 256: 4 wavefronts, one per SIMD (the O and Q operands alone take 192).
-  static constexpr int THREADS = DP <= 128 ? 512 : 256;
+  // Rows per wavefront: 32 (32x32x16 MFMAs) or 16 (16x16x32 MFMAs).
+  static constexpr int RW = RW_;
+  // 32 rows: head_dim 128: 8 wavefronts, two per SIMD (256 registers each);
+  // head_dim 256: 4 wavefronts, one per SIMD (the O and Q operands alone take
+  // 192).  16 rows at head_dim 256: 8 wavefronts, two per SIMD (O and Q take
+  // 96): one wavefront issues MFMAs at half the pipe's rate, two fill it.
+  static constexpr int THREADS = RW == 32 ? (DP <= 128 ? 512 : 256) : (DP <= 128 ? 1024 : 512);
   static constexpr int WAVES = THREADS / 64;
-  static constexpr int ROWS = 32 * WAVES;          // q rows per item (32 per wavefront)
+  static constexpr int ROWS = RW * WAVES;          // q rows per item
   static constexpr int ROWB = 2 * DP;              // bytes of one key's K (or V) row
   static constexpr int BK = 16384 / ROWB;          // keys per tile: 16 KiB of K, 16 KiB of V
   static constexpr int NSB = BK / 32;              // 32-key sub-blocks per tile
@@ -59,8 +63,8 @@ struct DmaCfg {
   static constexpr int CHUNKS = TILE / 1024;       // 1-KiB copies per K (or V) tile
   static constexpr int CPW = CHUNKS / WAVES;       // per wavefront
   static constexpr int CPR = ROWB / 16;            // 16-byte chunks per row
-  static constexpr int KSTEPS = DP / 16;           // QK^T k-steps
-  static constexpr int NT = DP / 32;               // 32-dim output blocks
+  static constexpr int KSTEPS = DP / (512 / RW);   // QK^T k-steps (16 or 32 dims each)
+  static constexpr int NT = DP / RW;               // RW-dim output blocks
   static constexpr int PLAN_BYTES = static_cast<int>(sizeof(PlanCore) + sizeof(PlanRows));
   static_assert(CHUNKS % WAVES == 0 && NSB >= 1, "whole copies per wavefront");
   static_assert(PLAN_BYTES >= 4 * (kMaxDecodeSeqs + 1), "block prefix fits the plan scratch");
@@ -93,6 +97,16 @@ __device__ __forceinline__ float xmax32(float x) {
   const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false,
                                                   false);
   return __builtin_fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float xmax16(float x) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false,
+                                                  false);
+  return __builtin_fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float xsum16(float x) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false,
+                                                  false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 __device__ __forceinline__ float xsum32(float x) {
   const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false,
@@ -167,9 +181,9 @@ __device__ __forceinline__ int32_t longest_first_block(const Params& p, const in
 // never rescaled.  At head_dim 256 that keeps the compiler from moving the
 // 128 accumulator registers between AGPRs and VGPRs on every tile (the rescale
 // is a VALU use of them); results equal the rescaling kernel's up to rounding.
-template <int DP_, typename OutS, bool CAP, bool FIXREF = false>
-__global__ void __launch_bounds__(DmaCfg<DP_>::THREADS)
-__attribute__((amdgpu_waves_per_eu(DP_ <= 128 ? 2 : 1)))
+template <int DP_, typename OutS, bool CAP, bool FIXREF = false, int RW_ = 32>
+__global__ void __launch_bounds__((DmaCfg<DP_, RW_>::THREADS))
+__attribute__((amdgpu_waves_per_eu((DmaCfg<DP_, RW_>::THREADS) / 256)))
 prefill_dma_kernel(Params p, const uint16_t* __restrict__ q, const uint16_t* __restrict__ keys,
                    const uint16_t* __restrict__ values, uint16_t* __restrict__ cache,
                    const int32_t* __restrict__ kv_lens, const int32_t* __restrict__ page_indices,
@@ -177,8 +191,10 @@ prefill_dma_kernel(Params p, const uint16_t* __restrict__ q, const uint16_t* __r
                    OutS* __restrict__ out, const int32_t* __restrict__ plan,
                    const float* __restrict__ part_o, const float* __restrict__ part_ml,
                    int32_t nfm, int32_t nfw) {
-  using C = DmaCfg<DP_>;
-  constexpr int DP = C::DP, BK = C::BK;
+  using C = DmaCfg<DP_, RW_>;
+  constexpr int DP = C::DP, BK = C::BK, RW = C::RW;
+  static_assert(RW == 32 || C::THREADS <= 512, "the plan scan's reduction slots hold 8 waves");
+  using Acc = typename std::conditional<RW == 32, f32x16_t, f32x4_t>::type;
   // Separate arrays per buffer: reads of one are never ordered after copies
   // into another.
   __shared__ __align__(1024) unsigned char kt0[C::TILE], kt1[C::TILE], kt2[C::TILE];
@@ -194,6 +210,9 @@ prefill_dma_kernel(Params p, const uint16_t* __restrict__ q, const uint16_t* __r
   const int wave = tid >> 6;
   const int col = lane & 31;
   const int half = lane >> 5;
+  // 16-row blocks: lane = 16 g + rn holds row rn (k-slots / output rows 4g ..).
+  const int rn = lane & 15;
+  const int g4l = lane >> 4;
   const bool decode_on = p.decode_waves > 0;
   const int32_t bq = C::ROWS / p.qpk;
   // ---- finish workgroups: [0, nfm) merge items, the last nfw write items.
@@ -246,7 +265,7 @@ prefill_dma_kernel(Params p, const uint16_t* __restrict__ q, const uint16_t* __r
   }
   const int32_t ntiles = hi > lo ? (hi - lo + BK - 1) / BK : 0;
 
-  const int32_t r = wave * 32 + col;
+  const int32_t r = wave * RW + (RW == 32 ? col : rn);
   const int32_t ti = r / p.qpk;
   const bool row_ok = ti < ntok && r < bq * p.qpk;
   const int32_t tok = tok0 + min(ti, ntok - 1);
@@ -262,9 +281,9 @@ prefill_dma_kernel(Params p, const uint16_t* __restrict__ q, const uint16_t* __r
   };
   int32_t row_lo, row_hi;
   key_range(tok, &row_lo, &row_hi);
-  const bool wave_live = wave * 32 < bq * p.qpk && wave * 32 / p.qpk < ntok;
-  const int32_t wt0 = tok0 + min(wave * 32 / p.qpk, ntok - 1);
-  const int32_t wt1 = tok0 + min(min(wave * 32 + 31, bq * p.qpk - 1) / p.qpk, ntok - 1);
+  const bool wave_live = wave * RW < bq * p.qpk && wave * RW / p.qpk < ntok;
+  const int32_t wt0 = tok0 + min(wave * RW / p.qpk, ntok - 1);
+  const int32_t wt1 = tok0 + min(min(wave * RW + RW - 1, bq * p.qpk - 1) / p.qpk, ntok - 1);
   int32_t w_lo0, w_hi0, w_lo1, w_hi1;
   key_range(wt0, &w_lo0, &w_hi0);
   key_range(wt1, &w_lo1, &w_hi1);
@@ -326,7 +345,8 @@ prefill_dma_kernel(Params p, const uint16_t* __restrict__ q, const uint16_t* __r
     const uint16_t* qrow = q + (static_cast<int64_t>(q_start + tok) * p.Hq + qhead) * DP;
 #pragma unroll
     for (int kk = 0; kk < C::KSTEPS; ++kk)
-      qop[kk] = *reinterpret_cast<const uint4*>(qrow + 16 * kk + 8 * half);
+      qop[kk] = *reinterpret_cast<const uint4*>(
+          qrow + (RW == 32 ? 16 * kk + 8 * half : 32 * kk + 8 * g4l));
   }
 
   // Swizzled operand offsets (ROWB-byte rows).  K: key 32 sb + col, chunk
@@ -343,17 +363,129 @@ prefill_dma_kernel(Params p, const uint16_t* __restrict__ q, const uint16_t* __r
 
   const float cm = CAP ? 1.0f : p.score_scale * kLog2e;
   const SoftCapLog2 capk = soft_cap_log2_consts(p);
-  f32x16_t oacc[C::NT];
+  Acc oacc[C::NT];
 #pragma unroll
-  for (int t = 0; t < C::NT; ++t) oacc[t] = f32x16_t{};
+  for (int t = 0; t < C::NT; ++t) oacc[t] = Acc{};
   float m_ref = -INFINITY;
   float l_run = 0.0f;
 
+  // ---- 16-row blocks (16x16x32 MFMAs).  Lane 16 g + rn: row rn.  Per 32-key
+  // sub-block: S^T for key groups x = 0, 1 (keys 32 sb + 16 x + ...):
+  //   A = K[key 32 sb + 16 x + rn][dims 32 kk + 8 g ..], B = Q^T (qop[kk]),
+  //   lane holds S^T[key 32 sb + 16 x + 4 g + i][row rn], i < 4;
+  // P^T k-slot 8 g + 4 x + i <-> key 32 sb + 16 x + 4 g + i, and the V^T
+  // operand (two ds_read_b64_tr_b16, x = 0, 1) follows the same key order:
+  //   A = V^T[dims 16 tt + rn][those 8 keys]; O^T[dim 16 tt + 4 g + i][row rn].
+  // K chunk c of key k at c ^ (k & 15); V chunk c at c ^ 4 (k & 3).
+  auto compute16 = [&](int32_t t, const unsigned char* kbuf, const unsigned char* vbuf,
+                       int32_t k0, bool need_mask) __attribute__((always_inline)) {
+    if constexpr (RW == 16) {
+#pragma unroll
+      for (int sb = 0; sb < C::NSB; ++sb) {
+        constexpr int KS = C::KSTEPS;
+        auto kread = [&](int x, int kk) __attribute__((always_inline)) -> uint4 {
+          const int key = 32 * sb + 16 * x + rn;
+          return *reinterpret_cast<const uint4*>(kbuf + key * C::ROWB +
+                                                 16 * ((4 * kk + g4l) ^ rn));
+        };
+        f32x4_t sacc[2] = {f32x4_t{}, f32x4_t{}};
+        constexpr int kRA = 4;  // K operand reads in flight (of 2 KS)
+        uint4 kb[kRA];
+#pragma unroll
+        for (int i = 0; i < kRA; ++i) kb[i] = kread(i & 1, i >> 1);
+#pragma unroll
+        for (int i = 0; i < 2 * KS; ++i) {
+          const uint4 kv = kb[i % kRA];
+          if (i + kRA < 2 * KS) kb[i % kRA] = kread((i + kRA) & 1, (i + kRA) >> 1);
+          sacc[i & 1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+              __builtin_bit_cast(bf16x8_t, kv), __builtin_bit_cast(bf16x8_t, qop[i >> 1]),
+              sacc[i & 1], 0, 0, 0);
+        }
+        // Scores: y[4 x + i] -> key k0 + 32 sb + 16 x + 4 g + i.
+        float y[8];
+#pragma unroll
+        for (int x = 0; x < 2; ++x)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            float v = sacc[x][i];
+            if constexpr (CAP) v = soft_cap_log2(v, capk.a, capk.b);
+            y[4 * x + i] = v;
+          }
+        float cme = cm;
+        if (!(cm > 0.0f)) {
+#pragma unroll
+          for (int i = 0; i < 8; ++i) y[i] *= cm;
+          cme = 1.0f;
+        }
+        if (need_mask) {
+#pragma unroll
+          for (int i = 0; i < 8; ++i) {
+            const int32_t j = k0 + 32 * sb + 16 * (i >> 2) + 4 * g4l + (i & 3);
+            if (j < row_lo || j >= row_hi) y[i] = -INFINITY;
+          }
+        }
+        float tmax = -INFINITY;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) tmax = __builtin_fmaxf(tmax, y[i]);
+        tmax = xmax32(xmax16(tmax));
+        const float m_tile = tmax * cme;
+        if constexpr (FIXREF) {
+          if (m_ref == -INFINITY && m_tile != -INFINITY)
+            m_ref = __builtin_fmaxf(m_tile, capk.b - 64.0f);
+        } else if (__any(m_tile > m_ref + kRescaleLog2)) {
+          const float m_new = __builtin_fmaxf(m_ref, m_tile);
+          const float alpha = (m_ref == -INFINITY) ? 0.0f : exp2f(m_ref - m_new);
+          l_run *= alpha;
+#pragma unroll
+          for (int tt = 0; tt < C::NT; ++tt) oacc[tt] *= alpha;
+          m_ref = m_new;
+        }
+        const float m_use = (m_ref == -INFINITY) ? 0.0f : m_ref;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) y[i] = __builtin_amdgcn_exp2f(fmaf(y[i], cme, -m_use));
+        const uint4 pop = make_uint4(pack_bf16x2_rne(y[0], y[1]), pack_bf16x2_rne(y[2], y[3]),
+                                     pack_bf16x2_rne(y[4], y[5]), pack_bf16x2_rne(y[6], y[7]));
+        float psum = sum_bf16x2(pop.x, sum_bf16x2(pop.y, 0.0f));
+        psum = sum_bf16x2(pop.z, sum_bf16x2(pop.w, psum));
+        l_run += psum;
+        // V^T reads: in 16-lane group g, lane jl (= rn) points at key
+        // 32 sb + 16 x + 4 g + jl / 4, dims 16 tt + 4 (jl & 3): chunk
+        // 2 tt + ((jl >> 1) & 1) at chunk ^ 4 (jl >> 2), byte 8 (jl & 1).
+        auto vread = [&](int tt) __attribute__((always_inline)) -> uint4 {
+          const int kq = 4 * g4l + (rn >> 2);
+          const int off = 16 * ((2 * tt + ((rn >> 1) & 1)) ^ (4 * (rn >> 2))) + 8 * (rn & 1);
+          const unsigned char* ra = vbuf + (32 * sb + kq) * C::ROWB + off;
+          const v4i16 va = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+              (__attribute__((address_space(3))) v4i16*)ra);
+          const v4i16 vb = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+              (__attribute__((address_space(3))) v4i16*)(ra + 16 * C::ROWB));
+          const uint2 ua = __builtin_bit_cast(uint2, va), ub = __builtin_bit_cast(uint2, vb);
+          return make_uint4(ua.x, ua.y, ub.x, ub.y);
+        };
+        constexpr int kVR = 2;
+        uint4 vb2[kVR];
+#pragma unroll
+        for (int i = 0; i < kVR; ++i) vb2[i] = vread(i);
+#pragma unroll
+        for (int tt = 0; tt < C::NT; ++tt) {
+          const uint4 vop = vb2[tt % kVR];
+          if (tt + kVR < C::NT) vb2[tt % kVR] = vread(tt + kVR);
+          oacc[tt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+              __builtin_bit_cast(bf16x8_t, vop), __builtin_bit_cast(bf16x8_t, pop), oacc[tt], 0,
+              0, 0);
+        }
+      }
+    }
+  };
   auto compute = [&](int32_t t, const unsigned char* kbuf, const unsigned char* vbuf)
                      __attribute__((always_inline)) {
     const int32_t k0 = lo + t * BK;
     if (!(wave_live && k0 < w_hi1 && k0 + BK > w_lo0)) return;
     const bool need_mask = !(k0 >= w_lo1 && k0 + BK <= w_hi0);
+    if constexpr (RW == 16) {
+      compute16(t, kbuf, vbuf, k0, need_mask);
+      return;
+    } else {
 #pragma unroll
     for (int sb = 0; sb < C::NSB; ++sb) {
       constexpr int kRA = 4;  // K operand reads in flight
@@ -462,6 +594,7 @@ prefill_dma_kernel(Params p, const uint16_t* __restrict__ q, const uint16_t* __r
       }
       __builtin_amdgcn_sched_group_barrier(0x008, 2, 1);
     }
+    }
   };
 
   // ---- pipeline.  Prologue: address tables of tiles 0..2, copies of tiles
@@ -503,21 +636,20 @@ prefill_dma_kernel(Params p, const uint16_t* __restrict__ q, const uint16_t* __r
     if (t + 2 < ntiles) iter(t + 2, kt2, vt2, ko1, vo1);
   }
 
-  // ---- output: lane l, block tt, register i -> dim 32 tt + 8 (i / 4) + 4 half + i % 4.
-  const float lsum = xsum32(l_run);
-  if (!row_ok) return;
-  const float lsum_s = sum_with_sink(p, qhead, m_ref, lsum);
-  const float inv = lsum_s > 0.0f ? p.v_scale / lsum_s : 0.0f;
-  const int64_t orow_i = static_cast<int64_t>(q_start + tok) * p.Hq + qhead;
-  if (p.lse != nullptr && half == 0) p.lse[orow_i] = lse_from_log2(m_ref, lsum);
-  OutS* orow = out + orow_i * DP;
+  if constexpr (RW == 16) {
+    // ---- output: lane 16 g + rn, block tt, register i -> dim 16 tt + 4 g + i.
+    const float lsum = xsum32(xsum16(l_run));
+    if (!row_ok) return;
+    const float lsum_s = sum_with_sink(p, qhead, m_ref, lsum);
+    const float inv = lsum_s > 0.0f ? p.v_scale / lsum_s : 0.0f;
+    const int64_t orow_i = static_cast<int64_t>(q_start + tok) * p.Hq + qhead;
+    if (p.lse != nullptr && g4l == 0) p.lse[orow_i] = lse_from_log2(m_ref, lsum);
+    OutS* orow = out + orow_i * DP;
 #pragma unroll
-  for (int tt = 0; tt < C::NT; ++tt)
-#pragma unroll
-    for (int g4 = 0; g4 < 4; ++g4) {
-      const int d = 32 * tt + 8 * g4 + 4 * half;
-      const float v0 = oacc[tt][4 * g4 + 0] * inv, v1 = oacc[tt][4 * g4 + 1] * inv;
-      const float v2 = oacc[tt][4 * g4 + 2] * inv, v3 = oacc[tt][4 * g4 + 3] * inv;
+    for (int tt = 0; tt < C::NT; ++tt) {
+      const int d = 16 * tt + 4 * g4l;
+      const float v0 = oacc[tt][0] * inv, v1 = oacc[tt][1] * inv;
+      const float v2 = oacc[tt][2] * inv, v3 = oacc[tt][3] * inv;
       if constexpr (sizeof(OutS) == 4) {
         *reinterpret_cast<float4*>(orow + d) = make_float4(v0, v1, v2, v3);
       } else {
@@ -528,4 +660,32 @@ prefill_dma_kernel(Params p, const uint16_t* __restrict__ q, const uint16_t* __r
                            (static_cast<uint32_t>(f32_to_bf16_bits(v3)) << 16));
       }
     }
+    return;
+  } else {
+    // ---- output: lane l, block tt, register i -> dim 32 tt + 8 (i / 4) + 4 half + i % 4.
+    const float lsum = xsum32(l_run);
+    if (!row_ok) return;
+    const float lsum_s = sum_with_sink(p, qhead, m_ref, lsum);
+    const float inv = lsum_s > 0.0f ? p.v_scale / lsum_s : 0.0f;
+    const int64_t orow_i = static_cast<int64_t>(q_start + tok) * p.Hq + qhead;
+    if (p.lse != nullptr && half == 0) p.lse[orow_i] = lse_from_log2(m_ref, lsum);
+    OutS* orow = out + orow_i * DP;
+#pragma unroll
+    for (int tt = 0; tt < C::NT; ++tt)
+#pragma unroll
+      for (int g4 = 0; g4 < 4; ++g4) {
+        const int d = 32 * tt + 8 * g4 + 4 * half;
+        const float v0 = oacc[tt][4 * g4 + 0] * inv, v1 = oacc[tt][4 * g4 + 1] * inv;
+        const float v2 = oacc[tt][4 * g4 + 2] * inv, v3 = oacc[tt][4 * g4 + 3] * inv;
+        if constexpr (sizeof(OutS) == 4) {
+          *reinterpret_cast<float4*>(orow + d) = make_float4(v0, v1, v2, v3);
+        } else {
+          *reinterpret_cast<uint2*>(orow + d) =
+              make_uint2(static_cast<uint32_t>(f32_to_bf16_bits(v0)) |
+                             (static_cast<uint32_t>(f32_to_bf16_bits(v1)) << 16),
+                         static_cast<uint32_t>(f32_to_bf16_bits(v2)) |
+                             (static_cast<uint32_t>(f32_to_bf16_bits(v3)) << 16));
+        }
+      }
+  }
 }
