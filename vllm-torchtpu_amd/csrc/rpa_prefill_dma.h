@@ -28,6 +28,8 @@
 //       V: chunk c of key k sits at chunk c ^ 4 (k & 3): a transposing read
 //          takes 4 keys x 2 chunks per 16-lane group, 4 aligned chunks per
 //          32 lanes; the XOR moves each key's 4 chunks to a distinct group of 4.
+//          16-row blocks read 8 keys x 2 chunks per 32 lanes and add 2 to the
+//          XOR for keys 4 .. 7 of each 8 (c ^ (4 (k & 3) + 2 ((k >> 2) & 1))).
 //     The swizzle is applied on the global side of the copy (lane l of a copy
 //     loads the global chunk that belongs at its fixed LDS slot).
 //   * One barrier per tile; the copies are issued as inline asm and waited for
@@ -319,6 +321,12 @@ prefill_dma_kernel(Params p, const uint16_t* __restrict__ q, const uint16_t* __r
       ktab[slot][tid][1] = reinterpret_cast<uint64_t>(vr);
     }
   };
+  // V chunk c of key k sits at chunk c ^ vswz(k).  16-row blocks read 8 keys
+  // (2 chunks each) per 32 lanes: bit 1 of the XOR separates keys 4 .. 7 of
+  // each 8 from keys 0 .. 3, so the 32 lanes cover all 64 banks.
+  auto vswz = [](int key) __attribute__((always_inline)) -> int {
+    return RW == 32 ? 4 * (key & 3) : 4 * (key & 3) + 2 * ((key >> 2) & 1);
+  };
   // ---- copies of tile t into buffer B: this wavefront's 1-KiB chunks
   // c = wave + WAVES i hold keys 4c .. 4c + 3; lane l lands at chunk l % 16 of
   // key 4c + l / 16 and loads the global chunk the swizzle puts there.
@@ -334,7 +342,7 @@ prefill_dma_kernel(Params p, const uint16_t* __restrict__ q, const uint16_t* __r
       const uint32_t kl = __builtin_amdgcn_readfirstlane(kbuf + 1024 * c);
       const uint32_t vl = __builtin_amdgcn_readfirstlane(vbuf + 1024 * c);
       dma16(ka + 16 * (j ^ (key & 15)), kl);
-      dma16(va + 16 * (j ^ (4 * (key & 3))), vl);
+      dma16(va + 16 * (j ^ vswz(key)), vl);
     }
   };
 
@@ -376,7 +384,7 @@ prefill_dma_kernel(Params p, const uint16_t* __restrict__ q, const uint16_t* __r
   // P^T k-slot 8 g + 4 x + i <-> key 32 sb + 16 x + 4 g + i, and the V^T
   // operand (two ds_read_b64_tr_b16, x = 0, 1) follows the same key order:
   //   A = V^T[dims 16 tt + rn][those 8 keys]; O^T[dim 16 tt + 4 g + i][row rn].
-  // K chunk c of key k at c ^ (k & 15); V chunk c at c ^ 4 (k & 3).
+  // K chunk c of key k at c ^ (k & 15); V chunk c at c ^ vswz(k).
   auto compute16 = [&](int32_t t, const unsigned char* kbuf, const unsigned char* vbuf,
                        int32_t k0, bool need_mask) __attribute__((always_inline)) {
     if constexpr (RW == 16) {
@@ -450,10 +458,10 @@ prefill_dma_kernel(Params p, const uint16_t* __restrict__ q, const uint16_t* __r
         l_run += psum;
         // V^T reads: in 16-lane group g, lane jl (= rn) points at key
         // 32 sb + 16 x + 4 g + jl / 4, dims 16 tt + 4 (jl & 3): chunk
-        // 2 tt + ((jl >> 1) & 1) at chunk ^ 4 (jl >> 2), byte 8 (jl & 1).
+        // 2 tt + ((jl >> 1) & 1) at chunk ^ vswz(key), byte 8 (jl & 1).
         auto vread = [&](int tt) __attribute__((always_inline)) -> uint4 {
           const int kq = 4 * g4l + (rn >> 2);
-          const int off = 16 * ((2 * tt + ((rn >> 1) & 1)) ^ (4 * (rn >> 2))) + 8 * (rn & 1);
+          const int off = 16 * ((2 * tt + ((rn >> 1) & 1)) ^ vswz(kq)) + 8 * (rn & 1);
           const unsigned char* ra = vbuf + (32 * sb + kq) * C::ROWB + off;
           const v4i16 va = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
               (__attribute__((address_space(3))) v4i16*)ra);
