@@ -426,10 +426,14 @@ prefill_dma_kernel(Params p, const uint16_t* __restrict__ q, const uint16_t* __r
           cme = 1.0f;
         }
         if (need_mask) {
+          // Key j = jb + c with a compile-time c: compare c against the
+          // range shifted by jb (no per-score offset registers).
+          const int32_t jb = k0 + 32 * sb + 4 * g4l;
+          const int32_t dlo = row_lo - jb, dhi = row_hi - jb;
 #pragma unroll
           for (int i = 0; i < 8; ++i) {
-            const int32_t j = k0 + 32 * sb + 16 * (i >> 2) + 4 * g4l + (i & 3);
-            if (j < row_lo || j >= row_hi) y[i] = -INFINITY;
+            const int32_t c = 16 * (i >> 2) + (i & 3);
+            if (c < dlo || c >= dhi) y[i] = -INFINITY;
           }
         }
         float tmax = -INFINITY;
@@ -494,8 +498,12 @@ prefill_dma_kernel(Params p, const uint16_t* __restrict__ q, const uint16_t* __r
       compute16(t, kbuf, vbuf, k0, need_mask);
       return;
     } else {
-#pragma unroll
-    for (int sb = 0; sb < C::NSB; ++sb) {
+    // One 32-key sub-block; sb is a compile-time constant so that each
+    // sub-block's scheduling groups get SyncIDs of their own.
+    auto sub_block = [&](auto sbc) __attribute__((always_inline)) {
+      constexpr int sb = decltype(sbc)::value;
+      constexpr int kSyncS = 2 * sb, kSyncPV = 2 * sb + 1;
+      __builtin_amdgcn_sched_barrier(0);
       constexpr int kRA = 4;  // K operand reads in flight
       auto kread = [&](int kk) __attribute__((always_inline)) -> uint4 {
         return *reinterpret_cast<const uint4*>(kbuf + 32 * C::ROWB * sb + (kbase ^ (32u * kk)));
@@ -512,13 +520,13 @@ prefill_dma_kernel(Params p, const uint16_t* __restrict__ q, const uint16_t* __r
             __builtin_bit_cast(bf16x8_t, kv), __builtin_bit_cast(bf16x8_t, qop[kk]), sacc, 0, 0,
             0);
       }
-      __builtin_amdgcn_sched_group_barrier(0x100, kRA, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, kRA, kSyncS);
 #pragma unroll
       for (int i = 0; i < C::KSTEPS - kRA; ++i) {
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, kSyncS);
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, kSyncS);
       }
-      __builtin_amdgcn_sched_group_barrier(0x008, kRA, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, kRA, kSyncS);
       // Scores: register i -> key k0 + 32 sb + 8 (i / 4) + 4 half + i % 4.
       float y[16];
 #pragma unroll
@@ -534,10 +542,14 @@ prefill_dma_kernel(Params p, const uint16_t* __restrict__ q, const uint16_t* __r
         cme = 1.0f;
       }
       if (need_mask) {
+        // Key j = jb + c with a compile-time c: compare c against the range
+        // shifted by jb (no per-score offset registers).
+        const int32_t jb = k0 + 32 * sb + 4 * half;
+        const int32_t dlo = row_lo - jb, dhi = row_hi - jb;
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
-          const int32_t j = k0 + 32 * sb + 8 * (i >> 2) + 4 * half + (i & 3);
-          if (j < row_lo || j >= row_hi) y[i] = -INFINITY;
+          const int32_t c = 8 * (i >> 2) + (i & 3);
+          if (c < dlo || c >= dhi) y[i] = -INFINITY;
         }
       }
       float tmax = -INFINITY;
@@ -594,14 +606,17 @@ prefill_dma_kernel(Params p, const uint16_t* __restrict__ q, const uint16_t* __r
             __builtin_bit_cast(bf16x8_t, vop), __builtin_bit_cast(bf16x8_t, pops[i / C::NT]),
             oacc[tt], 0, 0, 0);
       }
-      __builtin_amdgcn_sched_group_barrier(0x100, 4, 1);
+      __builtin_amdgcn_sched_group_barrier(0x100, 4, kSyncPV);
 #pragma unroll
       for (int i = 0; i < kP - 2; ++i) {
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);
-        __builtin_amdgcn_sched_group_barrier(0x100, 2, 1);
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, kSyncPV);
+        __builtin_amdgcn_sched_group_barrier(0x100, 2, kSyncPV);
       }
-      __builtin_amdgcn_sched_group_barrier(0x008, 2, 1);
-    }
+      __builtin_amdgcn_sched_group_barrier(0x008, 2, kSyncPV);
+    };
+    static_assert(C::NSB <= 2, "sub-blocks per tile");
+    sub_block(std::integral_constant<int, 0>{});
+    if constexpr (C::NSB > 1) sub_block(std::integral_constant<int, 1>{});
     }
   };
 
