@@ -144,14 +144,26 @@ __device__ __forceinline__ void write_record(const Params& p, E* __restrict__ ca
   const int64_t src_row = static_cast<int64_t>(t) * p.Hkv * p.D;
   const int32_t per_head = p.Dp / EPP;
   const int32_t pieces = p.Kx2 * per_head;
-  for (int32_t i = lane; i < pieces; i += 64) {
-    const int32_t c = i / per_head;
-    const int32_t e0 = (i - c * per_head) * EPP;
-    uint2 v = make_uint2(0u, 0u);
-    if (c < 2 * p.Hkv && e0 < p.D)
-      v = *reinterpret_cast<const uint2*>(((c & 1) ? values : keys) + src_row +
-                                          static_cast<int64_t>(c >> 1) * p.D + e0);
-    *reinterpret_cast<uint2*>(rec + static_cast<int64_t>(c) * p.Dp + e0) = v;
+  // Batches of kBatch pieces per lane: all loads, then all stores (one memory
+  // round trip per batch instead of one per piece).
+  constexpr int kBatch = 8;
+  for (int32_t i0 = lane; i0 < pieces; i0 += 64 * kBatch) {
+    uint2 v[kBatch];
+    int32_t dst[kBatch];
+#pragma unroll
+    for (int b = 0; b < kBatch; ++b) {
+      const int32_t i = i0 + 64 * b;
+      const int32_t c = i / per_head;
+      const int32_t e0 = (i - c * per_head) * EPP;
+      v[b] = make_uint2(0u, 0u);
+      dst[b] = i < pieces ? c * p.Dp + e0 : -1;
+      if (i < pieces && c < 2 * p.Hkv && e0 < p.D)
+        v[b] = *reinterpret_cast<const uint2*>(((c & 1) ? values : keys) + src_row +
+                                               static_cast<int64_t>(c >> 1) * p.D + e0);
+    }
+#pragma unroll
+    for (int b = 0; b < kBatch; ++b)
+      if (dst[b] >= 0) *reinterpret_cast<uint2*>(rec + dst[b]) = v[b];
   }
 }
 
