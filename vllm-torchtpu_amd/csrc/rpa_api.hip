@@ -49,6 +49,7 @@ rpa::Params make_params(const rpa_desc* d) {
   p.score_scale = d->sm_scale * d->k_scale * d->q_scale;
   p.v_scale = d->v_scale;
   p.rec = static_cast<int64_t>(d->kv_heads_x2) * d->head_dim_padded;
+  p.kv_bytes = dtype_bytes(d->kv_dtype);
   p.skip_kv_update = d->skip_kv_update ? 1 : 0;
   p.ps_shift = -1;
   for (int sh = 0; sh < 31; ++sh)

@@ -37,6 +37,7 @@ struct Params {
   int32_t decode_waves;    // wavefronts of the decode kernel's persistent grid (0: no decode kernel)
   int32_t prefill_on;      // the prefill kernel attends the non-decode rows
   int32_t dq;              // largest q_len of a decode row group (>= 1; dq * qpk <= 16)
+  int32_t kv_bytes;        // bytes per cache element (2: bf16, 1: fp8)
   float* lse;              // [T, Hq] natural-log LSE of each output row, or null
   const float* sink;       // [Hq] attention-sink logits (natural log), or null
 };

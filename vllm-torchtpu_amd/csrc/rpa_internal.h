@@ -69,11 +69,17 @@ hipError_t launch_decode(const Params& p, int kv_dtype, int out_dtype, const Dec
 // Prefill kernel: MFMA attention of every row the decode kernel does not
 // take (new tokens read from k/v), plus, in finish workgroups appended to its
 // grid, the finish kernel's merge and write items (the finish kernel is then
-// not launched) -- at padded head_dim <= 128.  At 256 the finish kernel runs
-// after it with the merge and write items.
+// not launched) -- at padded head_dim <= 128, and in the LDS-DMA kernel (bf16
+// KV, head_dim 128 or 256, unpadded).  Otherwise the finish kernel runs after
+// it with the merge and write items.
 template <int DP>
 constexpr bool kPrefillFinishRoles = DP <= 128;
-inline bool prefill_has_finish_roles(const Params& p) { return p.Dp <= 128; }
+inline bool prefill_dma_path(const Params& p) {
+  return p.kv_bytes == 2 && p.D == p.Dp && (p.Dp == 128 || p.Dp == 256);
+}
+inline bool prefill_has_finish_roles(const Params& p) {
+  return p.Dp <= 128 || prefill_dma_path(p);
+}
 bool prefill_supported(const Params& p, int q_dtype, int kv_dtype, int out_dtype);
 int prefill_merge_blocks(const Params& p, int num_cus);
 int prefill_write_blocks(const Params& p, int num_cus);

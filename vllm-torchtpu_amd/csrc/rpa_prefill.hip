@@ -634,7 +634,7 @@ hipError_t launch_dp(const Params& p, const void* q, const void* k, const void* 
   const bool full = p.D == p.Dp;
   if constexpr (sizeof(E) == 2) {
     // bf16 KV at head_dim 128 and 256: the LDS-DMA kernel (rpa_prefill_dma.h).
-    if ((p.Dp == 128 || p.Dp == 256) && full) {
+    if (prefill_dma_path(p)) {
 #define RPA_DMA_LAUNCH16(DPV, CAP, FIX)                                                          \
   hipLaunchKernelGGL((prefill_dma_kernel<DPV, OutS, CAP, FIX, 16>), g,                           \
                      dim3(DmaCfg<DPV, 16>::THREADS), 0, stream, p,                               \

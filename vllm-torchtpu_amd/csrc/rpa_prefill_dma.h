@@ -220,8 +220,7 @@ prefill_dma_kernel(Params p, const uint16_t* __restrict__ q, const uint16_t* __r
   // ---- finish workgroups: [0, nfm) merge items, the last nfw write items.
   const int32_t blk_id = static_cast<int32_t>(blockIdx.x);
   const int32_t nattn = static_cast<int32_t>(gridDim.x) - nfm - nfw;
-  // At head_dim 256 the finish kernel does this work (nfm = nfw = 0).
-  if constexpr (kPrefillFinishRoles<DP>) {
+  {
     if (blk_id < nfm || blk_id >= nfm + nattn) {
       const bool merges = blk_id < nfm;
       prefill_finish_role<uint16_t, DP, OutS>(p, aux, keys, values, cache, kv_lens,
