@@ -719,9 +719,11 @@ int prefill_merge_blocks(const Params& p, int num_cus) {
 }
 
 // Write workgroups (end of the grid): about 16 token rows each, at most one
-// per CU.
+// per CU.  The LDS-DMA kernel needs none: each attention workgroup writes its
+// own block's new tokens for its kv head.
 int prefill_write_blocks(const Params& p, int num_cus) {
-  if (p.skip_kv_update || p.T == 0 || !prefill_has_finish_roles(p)) return 0;
+  if (p.skip_kv_update || p.T == 0 || !prefill_has_finish_roles(p) || prefill_dma_path(p))
+    return 0;
   int64_t b = (static_cast<int64_t>(p.T) + 15) / 16;
   return static_cast<int>(b > num_cus ? num_cus : b);
 }

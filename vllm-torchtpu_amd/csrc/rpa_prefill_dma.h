@@ -658,6 +658,48 @@ prefill_dma_kernel(Params p, const uint16_t* __restrict__ q, const uint16_t* __r
     if (t + 2 < ntiles) iter(t + 2, kt2, vt2, ko1, vo1);
   }
 
+  // ---- this item's new tokens into the cache (kernel.py:154-166): token
+  // rows tok0 .. tok0 + ntok - 1 of the sequence are keys new_start + tok0 ..,
+  // and this workgroup is the only one holding them for kv head h, so it
+  // writes their K and V rows from the inputs (16-byte chunks; all loads of a
+  // batch before its stores).  Overlaps other workgroups' MFMA work instead of
+  // running in write workgroups at the launch's tail.
+  if (new_from_input) {
+    constexpr int CH = DP / 8;  // 16-byte chunks per K (or V) row
+    constexpr int kB = 8;
+    const int32_t nchunk = ntok * 2 * CH;
+    for (int32_t c0 = tid; c0 < nchunk; c0 += C::THREADS * kB) {
+      uint4 v[kB];
+      int32_t pgv[kB];
+      int32_t rowj[kB], part[kB];
+#pragma unroll
+      for (int b = 0; b < kB; ++b) {
+        const int32_t c = c0 + b * C::THREADS;
+        const int32_t i = c / (2 * CH);
+        const int32_t r = c - i * 2 * CH;  // K chunks, then V chunks
+        const int32_t j = new_start + tok0 + i;
+        rowj[b] = (c < nchunk && j >= 0 && j < kv_cap) ? j : -1;
+        part[b] = r;
+        pgv[b] = -1;
+        v[b] = make_uint4(0u, 0u, 0u, 0u);
+        if (rowj[b] >= 0) {
+          pgv[b] = ptab[page_of(p, j)];
+          const uint16_t* src = (r < CH ? keys : values) +
+                                (static_cast<int64_t>(q_start + tok0 + i) * p.Hkv + h) * DP +
+                                8 * (r < CH ? r : r - CH);
+          v[b] = *reinterpret_cast<const uint4*>(src);
+        }
+      }
+#pragma unroll
+      for (int b = 0; b < kB; ++b) {
+        if (rowj[b] < 0 || pgv[b] < 0 || pgv[b] >= p.P) continue;
+        uint16_t* dst = cache + (static_cast<int64_t>(pgv[b]) * p.ps + slot_of(p, rowj[b])) * p.rec +
+                        static_cast<int64_t>(2 * h) * DP + 8 * part[b];
+        *reinterpret_cast<uint4*>(dst) = v[b];
+      }
+    }
+  }
+
   if constexpr (RW == 16) {
     // ---- output: lane 16 g + rn, block tt, register i -> dim 16 tt + 4 g + i.
     const float lsum = xsum32(xsum16(l_run));
