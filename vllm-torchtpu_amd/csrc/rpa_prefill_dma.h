@@ -4,13 +4,19 @@
 //
 // Included by rpa_prefill.hip, whose prefill_kernel it replaces for these
 // shapes.  The item decomposition, row layout and math are the same: a
-// workgroup of 8 wavefronts (4 at head_dim 256) owns 256 (128) q rows
-// (BQ = rows / qpk query tokens of one sequence times the qpk q heads of one
-// kv head), wavefront w owns rows
-// [32w, 32w + 32), lane l owns MFMA column l % 32, and per 32-key sub-block
+// workgroup of 8 wavefronts owns 256 q rows at head_dim 128 (BQ = rows / qpk
+// query tokens of one sequence times the qpk q heads of one kv head),
+// wavefront w owns rows [32w, 32w + 32), lane l owns MFMA column l % 32, and
+// per 32-key sub-block
 //   S^T[key, row] = K[key, :] . Q^T[:, row]          (v_mfma_f32_32x32x16_bf16)
 //   O^T[dim, row] += V^T[dim, key] . P^T[key, row]    (V^T via ds_read_b64_tr_b16)
-// with an online softmax in the column layout.
+// with an online softmax in the column layout.  At head_dim 256 the 8
+// wavefronts own 16 rows each (128 rows, v_mfma_f32_16x16x32_bf16): 32-row
+// blocks would need 192 registers for O and Q, i.e. one wavefront per SIMD.
+// Each attention workgroup also writes its q block's new K/V records for its
+// kv head into the cache (it is the only workgroup holding those tokens for
+// that head); merge workgroups at the front of the grid combine the decode
+// kernel's split-K partials.
 //
 // What changes is the tile path:
 //   * Three LDS tile buffers (16 KiB of K and 16 KiB of V each: 64 keys at
