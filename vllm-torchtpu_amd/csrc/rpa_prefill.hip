@@ -609,6 +609,12 @@ prefill_kernel(Params p, const uint16_t* __restrict__ q,
 
 #include "rpa_prefill_dma.h"
 
+// The grid below is sized with PrefillCfg's rows per item; the LDS-DMA
+// instances must cover the same rows per item.
+static_assert(DmaCfg<128>::ROWS == PrefillCfg<128>::ROWS &&
+                  DmaCfg<256, 16>::ROWS == PrefillCfg<256>::ROWS,
+              "LDS-DMA and register-staged kernels share the item size");
+
 template <typename KV, typename OutS>
 hipError_t launch_dp(const Params& p, const void* q, const void* k, const void* v, void* cache,
                      const int32_t* kv_lens, const int32_t* page_indices, const int32_t* cu,
