@@ -202,6 +202,30 @@ __device__ __forceinline__ void write_new_token(const Params& p, typename KV::st
   }
 }
 
+// The same from registers (unpadded head_dim): page id pg of position j, and
+// lane l < 2 DP EB / 16 holding bytes [16 l, 16 l + 16) of the token's K|V
+// chunk of kv head h (K then V, as in the record).
+template <typename KV, int DP>
+__device__ __forceinline__ void write_new_token_regs(const Params& p, typename KV::storage* cache,
+                                                     int32_t pg, int32_t h, int32_t j, uint4 v,
+                                                     int lane) {
+  using E = typename KV::storage;
+  constexpr int EPP = 8 / sizeof(E);  // elements per 8-byte piece
+  constexpr int PIECES = DP / EPP;    // pieces per head chunk
+  constexpr int NEWP = 2 * DP * sizeof(E) / 16;
+  if (pg < 0 || pg >= p.P) return;
+  E* rec = cache + (static_cast<int64_t>(pg) * p.ps + slot_of(p, j)) * p.rec;
+  if (lane < NEWP)
+    *reinterpret_cast<uint4*>(reinterpret_cast<unsigned char*>(rec + static_cast<int64_t>(2 * h) * DP) +
+                              16 * lane) = v;
+  if (h == p.Hkv - 1) {
+    const int32_t npad = (p.Kx2 - 2 * p.Hkv) * PIECES;
+    for (int i = lane; i < npad; i += 64)
+      *reinterpret_cast<uint2*>(rec + static_cast<int64_t>(2 * p.Hkv) * DP + i * EPP) =
+          make_uint2(0u, 0u);
+  }
+}
+
 // The same for a group's new tokens j0 <= j < j1 (input rows
 // tq0 + j - j0) for kv head h (kernel.py:154-166): combined heads 2h (K) and
 // 2h + 1 (V), head dims >= D zero; the wavefront of the last kv head also
@@ -403,16 +427,47 @@ decode_kernel(Params p, const uint16_t* __restrict__ q, const typename KV::stora
     }
   };
 
+  // New token of a one-token group (kernel.py:154-166, :634-641): its K|V
+  // bytes (HB = 2 * DP * EB, 16 bytes per lane for lanes < HB / 16: K, then
+  // V) and its page id, loaded with the pair's last tile one pipeline step
+  // ahead, so that the LDS patch and the cache write of the tile's owner
+  // wait on no load.  Unpadded head_dim only (the input rows are the record's
+  // chunks).
+  constexpr bool kPrefetchNew = !MULTI && FULL_D;
+  constexpr int NEWP = C::HB / 16;  // 16-byte pieces of the new token's K|V
+  static_assert(NEWP <= 64, "one piece per lane");
+  struct NewTok {
+    uint4 v;
+    int32_t pg;
+  };
+  auto load_new = [&](const TileInfo& ti, NewTok& nt) __attribute__((always_inline)) {
+    if constexpr (kPrefetchNew) {
+      if (write_kv && ti.lt + 1 == ti.nt) {
+        const int32_t sq = min(max(ti.s, 0), p.S - 1);
+        const int32_t j = ti.hi - 1;
+        nt.pg = page_indices[static_cast<int64_t>(sq) * p.pps + page_of(p, min(max(j, 0), max_tok))];
+        if (lane < NEWP) {
+          const int c = lane / (NEWP / 2);
+          const int64_t row = (static_cast<int64_t>(L.tq[sq]) * p.Hkv + ti.h) * DP;
+          const unsigned char* src = reinterpret_cast<const unsigned char*>((c ? values : keys) + row);
+          nt.v = *reinterpret_cast<const uint4*>(src + 16 * (lane - c * (NEWP / 2)));
+        }
+      }
+    }
+  };
+
   // ---- pipeline ----------------------------------------------------------------
   TileInfo cur = locate(g_begin);
   uint4 qbuf[2][KK];
   uint4 bufr[2][NOCT][NPART];
   Pages pbuf[2];
+  NewTok nbuf[2];
   pages_of(cur, pbuf[0]);
   // The plan's stores go out while the first page ids are in flight.
   publish_plan(p, pl, L, plan_ws);
   load_tile(cur, pbuf[0], bufr[0]);
   load_q(cur, qbuf[0]);
+  load_new(cur, nbuf[0]);
   TileInfo nxt = advance(cur);
   pages_of(nxt.g < g_end ? nxt : cur, pbuf[0]);
 
@@ -430,6 +485,7 @@ decode_kernel(Params p, const uint16_t* __restrict__ q, const typename KV::stora
   // every load is unconditional.  All buffers alternate between the two call
   // sites, so no register copy forces an early wait on a prefetch.
   auto step = [&](uint4 (*CB)[NPART], uint4 (*NB)[NPART], const uint4* CQ, uint4* NQ,
+                  const NewTok& CN, NewTok& NN,
                   const Pages& CP, Pages& NP) __attribute__((always_inline)) -> bool {
     const bool has_nxt = nxt.g < g_end;
     const TileInfo nn = has_nxt ? advance(nxt) : nxt;
@@ -437,6 +493,7 @@ decode_kernel(Params p, const uint16_t* __restrict__ q, const typename KV::stora
     pages_of(nn.g < g_end ? nn : ldt, NP);
     load_tile(ldt, CP, NB);
     load_q(ldt, NQ);
+    load_new(ldt, NN);
 
     const int32_t base = cur.lo + cur.lt * TT;
     const bool last_tile = cur.lt + 1 == cur.nt;
@@ -474,7 +531,11 @@ decode_kernel(Params p, const uint16_t* __restrict__ q, const typename KV::stora
         store_piece_bf16<KV>(buf + (8 * o + tl) * C::KS, pt * EPP + ol * (EPP / 8), CB[o][pt]);
     if (patch) {
       wave_lds_sync();
-      patch_rows<KV, DP>(buf, C::KS, pr0, pr1, knew, new_stride, p.D, lane);
+      if constexpr (kPrefetchNew) {
+        if (lane < NEWP / 2) store_piece_bf16<KV>(buf + pr0 * C::KS, lane * (16 / C::EB), CN.v);
+      } else {
+        patch_rows<KV, DP>(buf, C::KS, pr0, pr1, knew, new_stride, p.D, lane);
+      }
     }
     wave_lds_sync();
     f32x4_t sacc[NG];
@@ -566,7 +627,14 @@ decode_kernel(Params p, const uint16_t* __restrict__ q, const typename KV::stora
       }
     if (last_tile || patch) {
       wave_lds_sync();
-      if (patch) patch_rows<KV, DP>(buf, C::VS, pr0, pr1, vnew, new_stride, p.D, lane);
+      if (patch) {
+        if constexpr (kPrefetchNew) {
+          if (lane >= NEWP / 2 && lane < NEWP)
+            store_piece_bf16<KV>(buf + pr0 * C::VS, (lane - NEWP / 2) * (16 / C::EB), CN.v);
+        } else {
+          patch_rows<KV, DP>(buf, C::VS, pr0, pr1, vnew, new_stride, p.D, lane);
+        }
+      }
       if (last_tile) zero_rows<DP, TT>(buf, C::VS, cur.hi - base, lane);
     }
     wave_lds_sync();
@@ -597,6 +665,8 @@ decode_kernel(Params p, const uint16_t* __restrict__ q, const typename KV::stora
       if constexpr (MULTI)
         write_new_tokens<KV, DP>(p, cache, page_indices, keys, values, cur.s, cur.h, base + pr0,
                                  base + pr1, tq_new, lane);
+      else if constexpr (kPrefetchNew)
+        write_new_token_regs<KV, DP>(p, cache, CN.pg, cur.h, cur.hi - 1, CN.v, lane);
       else
         write_new_token<KV, DP>(p, cache, page_indices, keys, values, cur.s, cur.h, cur.hi - 1,
                                 tq_cur, lane);
@@ -648,8 +718,8 @@ decode_kernel(Params p, const uint16_t* __restrict__ q, const typename KV::stora
     return true;
   };
 
-  while (step(bufr[0], bufr[1], qbuf[0], qbuf[1], pbuf[0], pbuf[1]) &&
-         step(bufr[1], bufr[0], qbuf[1], qbuf[0], pbuf[1], pbuf[0])) {
+  while (step(bufr[0], bufr[1], qbuf[0], qbuf[1], nbuf[0], nbuf[1], pbuf[0], pbuf[1]) &&
+         step(bufr[1], bufr[0], qbuf[1], qbuf[0], nbuf[1], nbuf[0], pbuf[1], pbuf[0])) {
   }
 }
 
