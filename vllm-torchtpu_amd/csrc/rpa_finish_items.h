@@ -18,29 +18,46 @@
 
 namespace rpa {
 
-// Merge item `it` (pair index) with the decode kernel's published plan.
+// Merge item `it` (pair index, it < S * Hkv) with the decode kernel's
+// published plan.  The plan header (sequence count n, tiles per wavefront)
+// and the item's entries are loaded together -- one memory round trip before
+// the partials' -- and an empty asm that reads them all keeps the compiler
+// from sinking any of them below the tests.  Entries of sequences past n are
+// stale but inside the plan, and are discarded.  Returns false when the
+// item's sequence is past n (so is every later item's).
 template <int DP, typename OutS>
-__device__ __forceinline__ void finish_merge_item(const Params& p, const PlanView& pv, int32_t it,
+__device__ __forceinline__ bool finish_merge_item(const Params& p, const PlanView& pv, int32_t it,
                                                   const int32_t* __restrict__ cu,
                                                   const float* __restrict__ part_o,
                                                   const float* __restrict__ part_ml,
                                                   OutS* __restrict__ out) {
   const int32_t s = it / p.Hkv;
   const int32_t h = it - s * p.Hkv;
-  const int32_t tpw = max(pv.hdr[1], 1);
+  // (The header is indexed by a zero that an asm produces, so that its loads
+  // are not hoisted out of the caller's loop -- and waited on -- ahead of
+  // the item's loads.)
+  int32_t z = 0;
+  asm volatile("" : "+v"(z));
+  int32_t hn = pv.hdr[z], htpw = pv.hdr[z + 1];
+  int32_t b0 = pv.base[s], b1 = pv.base[s + 1], dkv = pv.dkv[s], tq = pv.tq[s];
+  int32_t c0 = cu[s], c1 = cu[s + 1];
+  asm volatile("" : "+v"(hn), "+v"(htpw), "+v"(b0), "+v"(b1), "+v"(dkv), "+v"(tq), "+v"(c0),
+               "+v"(c1));
+  const int32_t n = min(max(hn, 0), p.S);
+  const int32_t tpw = max(htpw, 1);
   // The pair's tiles [g0, g0 + nt) of the work line; the wavefronts owning
   // its first and last tile, and its partial slots w + pair.
-  const int32_t nt = pv.base[s + 1] - pv.base[s];
-  if (pv.dkv[s] == 0 || nt <= 0) return;
-  const int32_t g0 = p.Hkv * pv.base[s] + h * nt;
+  const int32_t nt = b1 - b0;
+  if (s >= n) return false;
+  if (dkv == 0 || nt <= 0) return true;
+  const int32_t g0 = p.Hkv * b0 + h * nt;
   const int32_t wa = g0 / tpw, wb = (g0 + nt - 1) / tpw;
-  if (wa == wb) return;  // one wavefront finished the pair
+  if (wa == wb) return true;  // one wavefront finished the pair
   const int32_t first = wa + it;
   const int32_t nparts = wb - wa + 1;
   // The decode group's rows: q_len tokens x qpk heads (q_len * qpk <= 16).
-  const int32_t ql = p.dq > 1 ? min(max(cu[s + 1] - cu[s], 1), p.dq) : 1;
+  const int32_t ql = p.dq > 1 ? min(max(c1 - c0, 1), p.dq) : 1;
   const int32_t rows = min(ql * p.qpk, 16);
-  const int32_t tq = pv.tq[s];
   switch (decode_slot_rows(p.qpk * p.dq)) {
     case 1: merge_partials<DP, 1>(p, part_o, part_ml, first, nparts, rows, out, tq, h); break;
     case 2: merge_partials<DP, 2>(p, part_o, part_ml, first, nparts, rows, out, tq, h); break;
@@ -48,6 +65,7 @@ __device__ __forceinline__ void finish_merge_item(const Params& p, const PlanVie
     case 8: merge_partials<DP, 8>(p, part_o, part_ml, first, nparts, rows, out, tq, h); break;
     default: merge_partials<DP, 16>(p, part_o, part_ml, first, nparts, rows, out, tq, h); break;
   }
+  return true;
 }
 
 // Sequence that owns token row t for the row items: with the decode kernel's

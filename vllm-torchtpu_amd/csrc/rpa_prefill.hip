@@ -155,6 +155,15 @@ __device__ __forceinline__ void prefill_finish_role(
   const int wave = threadIdx.x >> 6;
   const bool decode_on = p.decode_waves > 0;
   const PlanView pv = plan_view(plan, p.S);
+  const int32_t nw = nfin * pw;
+  if (merges) {
+    // Bounded by S * Hkv: each item loads the sequence count n with its own
+    // plan entries, and the loop ends at the first item past n.
+    if (!decode_on) return;
+    for (int32_t it = fb * pw + wave; it < p.S * p.Hkv; it += nw)
+      if (!finish_merge_item<DP, OutS>(p, pv, it, cu, part_o, part_ml, out)) break;
+    return;
+  }
   PlanCore& pl_core = *reinterpret_cast<PlanCore*>(smem);
   PlanRows* pl_rows = reinterpret_cast<PlanRows*>(smem + sizeof(PlanCore));
   int32_t n;
@@ -163,15 +172,10 @@ __device__ __forceinline__ void prefill_finish_role(
   } else {
     n = build_plan(p, kv_lens, cu, dist, 16, false, pl_core, pl_rows).num_seqs;
   }
-  const int32_t total = merges ? (decode_on ? n * p.Hkv : 0) : (p.skip_kv_update ? 0 : p.T);
-  const int32_t nw = nfin * pw;
-  for (int32_t it = fb * pw + wave; it < total; it += nw) {
-    if (merges)
-      finish_merge_item<DP, OutS>(p, pv, it, cu, part_o, part_ml, out);
-    else
-      finish_write_item<E>(p, decode_on, pv, pl_rows, n, cu, kv_lens, cache, page_indices, keys,
-                           values, it, lane);
-  }
+  const int32_t total = p.skip_kv_update ? 0 : p.T;
+  for (int32_t it = fb * pw + wave; it < total; it += nw)
+    finish_write_item<E>(p, decode_on, pv, pl_rows, n, cu, kv_lens, cache, page_indices, keys,
+                         values, it, lane);
 }
 
 // Two wavefronts per SIMD at head_dim 128 (256 registers per lane), one at 256.
