@@ -383,6 +383,23 @@ def test_decode_repeated_calls(gpu_device):
     check(W.make_workload(DECODE_EDGE, 32, 8, 128, 16, seed=37, name="decode-after"), gpu_device)
 
 
+def test_stale_plan_entries_past_num_seqs(gpu_device):
+    """Merge wavefronts load a pair's plan entries together with the plan's
+    sequence count, before they know whether the pair exists
+    (rpa_finish_items.h).  After a larger batch on the same workspace, the plan
+    slots past a smaller batch's num_seqs hold that batch's split pairs; they
+    must be discarded (kernel.py:1345-1349: only s < num_seqs exists).  The
+    stale pairs' output rows (token s of the larger batch) are checked rows of
+    a prefill sequence in the smaller batches, so a stale merge would show."""
+    big = W.make_workload([(1, k) for k in (3000, 2500, 4000, 1800, 3500, 2900, 3300, 2100)],
+                          32, 8, 128, 16, seed=41, max_num_seqs=8, name="stale-a")
+    check(big, gpu_device)
+    for seed, seqs in ((42, [(1, 2200), (1, 3900), (1, 60), (6, 300)]),
+                       (43, [(1, 700), (9, 500)])):
+        check(W.make_workload(seqs, 32, 8, 128, 16, seed=seed, max_num_seqs=8,
+                              name=f"stale-b{len(seqs)}"), gpu_device)
+
+
 def test_decode_only_measurement_path(gpu_device):
     """RPA_PATH_DECODE_ONLY launches the decode kernel alone: single-unit
     decode rows are final; shapes the decode kernel does not take are rejected."""
