@@ -354,11 +354,15 @@ def test_decode_head_dims(gpu_device, d):
     check(W.make_workload(DECODE_EDGE, 16, 8, d, 16, seed=33, name=f"decode-d{d}"), gpu_device)
 
 
-def test_decode_many_seqs(gpu_device):
+@pytest.mark.parametrize("n,kv_max,dt", [(300, 3000, BF16), (600, 600, BF16), (600, 600, E4M3)])
+def test_decode_many_seqs(gpu_device, n, kv_max, dt):
+    """600 sequences x 8 kv heads = 4800 pairs: more than the merge wavefronts of
+    the second launch (at most 512 workgroups x 8), so some merge more than one
+    pair -- bf16 in the LDS-DMA kernel, fp8 in the register-staged one."""
     g = torch.Generator().manual_seed(34)
-    kvl = torch.randint(1, 3000, (300,), generator=g).tolist()
-    check(W.make_workload([(1, k) for k in kvl], 32, 8, 128, 16, seed=34, name="decode-300"),
-          gpu_device)
+    kvl = torch.randint(1, kv_max, (n,), generator=g).tolist()
+    check(W.make_workload([(1, k) for k in kvl], 32, 8, 128, 16, kv_dtype=dt, seed=34,
+                          name=f"decode-{n}"), gpu_device)
 
 
 def test_decode_f32_out(gpu_device):
