@@ -121,6 +121,17 @@ def test_basic(gpu_device, path, ps):
     check(W.make_workload(BASIC, 32, 8, 128, ps, seed=1234, name="basic"), gpu_device, path)
 
 
+@pytest.mark.parametrize("dt", [BF16, E4M3])
+@pytest.mark.parametrize("q_len", [1, 5])
+@pytest.mark.parametrize("ps", [128, 256, 512])
+def test_large_page_sizes(gpu_device, ps, q_len, dt):
+    """correctness_test.py:470-520: page sizes 128-512 with kv_lens that are not
+    multiples of 128; q_len 1 takes the decode kernel, 5 the prefill kernel."""
+    seqs = [(q_len, n) for n in (18, 129, 597, 1107, 31, 1328)]
+    check(W.make_workload(seqs, 32, 8, 128, ps, kv_dtype=dt, seed=44,
+                          name=f"ps{ps}-q{q_len}"), gpu_device)
+
+
 @pytest.mark.parametrize("path", PATHS)
 @pytest.mark.parametrize("name,seqs", [("decode", DECODE16), ("prefill", PREFILL16),
                                        ("mixed", MIXED16)])
