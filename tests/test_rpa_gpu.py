@@ -398,6 +398,34 @@ def test_decode_repeated_calls(gpu_device):
     check(W.make_workload(DECODE_EDGE, 32, 8, 128, 16, seed=37, name="decode-after"), gpu_device)
 
 
+def test_decode_one_pair_many_partials(gpu_device):
+    """One long decode pair spread over nearly every decode wavefront (about 900
+    partials): the merge combines them 64 units at a time (rpa_merge.h)."""
+    check(W.make_workload([(1, 200000)], 8, 1, 128, 256, seed=46, name="one-pair"),
+          gpu_device)
+
+
+def test_1m_context(gpu_device):
+    """correctness_test.py:950-985: two decodes of 1M keys, head_dim 256, page size
+    256, max_num_seqs 192, distribution [2, 2, 2].  The 4.3 GB cache puts pages
+    past 4 GB, and each (sequence, kv head) pair is spread over about 256
+    wavefronts."""
+    kv = 1 << 20
+    w = W.make_workload([(1, kv)] * 2, 8, 2, 256, 256, seed=45, max_num_seqs=192,
+                        num_pages=2 * kv // 256 + 8, distribution=[2, 2, 2], name="1m-context")
+    check(w, gpu_device)
+
+
+def test_large_schedule(gpu_device):
+    """correctness_test.py:525-551: 1024 decodes, 16 q heads on one kv head (16 rows
+    per decode group), head_dim 256, page size 256.  The reference's 8191 keys per
+    sequence are cut to 2047 (a 2.1 GB cache) so that building the workload and
+    the CPU oracle take seconds, not most of a minute."""
+    w = W.make_workload([(1, 2047)] * 1024, 16, 1, 256, 256, seed=47,
+                        num_pages=8 * 1024 + 32, name="large-schedule")
+    check(w, gpu_device)
+
+
 def test_stale_plan_entries_past_num_seqs(gpu_device):
     """Merge wavefronts load a pair's plan entries together with the plan's
     sequence count, before they know whether the pair exists
