@@ -165,7 +165,11 @@ def assert_close(actual, expected, atol, rtol, what=""):
     assert a.shape == e.shape, (a.shape, e.shape)
     err = (a - e).abs()
     bound = atol + rtol * e.abs()
-    bad = err > bound
+    # NaN on one side only is a mismatch (err > bound is False for a NaN err), and
+    # so is an infinity the other side does not share (the bound is infinite
+    # there); NaN on both sides, or the same infinity, matches.
+    inf = torch.isinf(a) | torch.isinf(e)
+    bad = (err > bound) | (torch.isnan(a) != torch.isnan(e)) | (inf & (a != e))
     if bad.any():
         idx = bad.nonzero()[0].tolist()
         raise AssertionError(

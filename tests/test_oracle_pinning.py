@@ -612,3 +612,20 @@ def test_merge_nan_lse_propagates():
     o3, l3 = O.merge_attn_states(torch.stack([out_a, out_b]), torch.stack([lse_a, lse_b]))
     assert torch.equal(torch.isnan(o3), torch.isnan(o)) and torch.equal(torch.isnan(l3), torch.isnan(l))
 
+
+
+def test_assert_close_flags_one_sided_nan():
+    """The parity helper treats NaN on one side only as a mismatch (a NaN error
+    compares false against any bound), NaN on both sides and equal infinities as
+    matches."""
+    one = torch.tensor([1.0, 2.0])
+    with pytest.raises(AssertionError):
+        assert_close(torch.tensor([float("nan"), 2.0]), one, 1e-2, 1e-2, "nan vs finite")
+    with pytest.raises(AssertionError):
+        assert_close(one, torch.tensor([1.0, float("nan")]), 1e-2, 1e-2, "finite vs nan")
+    with pytest.raises(AssertionError):
+        assert_close(torch.tensor([float("inf")]), torch.tensor([-float("inf")]), 1e-2, 1e-2)
+    with pytest.raises(AssertionError):
+        assert_close(torch.tensor([3.0]), torch.tensor([float("inf")]), 1e-2, 1e-2)
+    assert_close(torch.tensor([float("nan"), float("inf")]),
+                 torch.tensor([float("nan"), float("inf")]), 1e-2, 1e-2, "matching")
