@@ -295,6 +295,58 @@ def test_nan_sequence_stays_in_its_rows(gpu_device):
     assert torch.isfinite(out[:3].float()).all() and torch.isfinite(out[4:].float()).all()
 
 
+def _check_dq(w, dev, q_len, what):
+    """Oracle against the GPU path with decode groups of q_len tokens
+    (decode_query_size is a scheduling choice: the oracle takes none)."""
+    exp_out, exp_cache = O.ref_ragged_paged_attention(*w.args(), mode="fp32", **w.kwargs)
+    out, cache = run_gpu(w, dev, decode_query_size=q_len)
+    tol = TOL[w.kv_cache.dtype]
+    assert_close(out, exp_out, tol, tol, f"{what} output")
+    assert bytes_equal(cache, exp_cache), f"{what}: cache differs from the oracle"
+    return out
+
+
+@pytest.mark.parametrize("q_len", [1, 4])
+def test_nan_cached_kv_stays_in_its_sequence(gpu_device, q_len):
+    """correctness_test.py:703-727: every cached K/V page of sequence 1 holds NaN;
+    only that sequence's rows may be NaN, and every other row equals the oracle
+    (decode groups of q_len tokens, all sequences on the decode path)."""
+    seqs = [(q_len, k) for k in (129, 597, 256, 512, 768, 256, 1024, 512)]
+    n = len(seqs)
+    w = W.make_workload(seqs, 32, 8, 128, 16, seed=48, distribution=[n, n, n],
+                        name=f"nan-kv-q{q_len}")
+    S = w.kv_lens.shape[0]
+    pps = w.page_indices.shape[0] // S
+    w.kv_cache[w.page_indices[pps:pps + O.cdiv(597, 16)].long()] = float("nan")
+    _log(f"[rpa-gpu] case {w.name}")
+    out = _check_dq(w, gpu_device, q_len, w.name)
+    assert torch.isnan(out[q_len:2 * q_len].float()).all()
+    assert torch.isfinite(out[:q_len].float()).all()
+    assert torch.isfinite(out[2 * q_len:].float()).all()
+
+
+@pytest.mark.parametrize("dt", [BF16, E4M3])
+@pytest.mark.parametrize("q_len", [1, 4])
+@pytest.mark.parametrize("d", [128, 256])
+def test_nan_new_kv_stays_in_its_sequence(gpu_device, d, q_len, dt):
+    """correctness_test.py:759-790: NaN new keys and values of one short decode
+    (sequence 128 / q_len of a batch of them, page size 256) reach only that
+    sequence's rows and its own cache slots."""
+    bad = 128 // q_len
+    seqs = [(q_len, 4 + q_len)] * (bad + 3)
+    n = len(seqs)
+    w = W.make_workload(seqs, 8, 2, d, 256, kv_dtype=dt, seed=49, distribution=[n, n, n],
+                        name=f"nan-new-d{d}-q{q_len}")
+    t0 = int(w.cu_q_lens[bad])
+    w.k[t0:t0 + q_len] = float("nan")
+    w.v[t0:t0 + q_len] = float("nan")
+    _log(f"[rpa-gpu] case {w.name} {dt}")
+    out = _check_dq(w, gpu_device, q_len, w.name)
+    assert torch.isnan(out[t0:t0 + q_len].float()).all()
+    assert torch.isfinite(out[:t0].float()).all()
+    assert torch.isfinite(out[t0 + q_len:].float()).all()
+
+
 def test_bundled_matches_flat(gpu_device):
     """test_rpa_bundled.py:173-227: bundled block-major == per-layer flat, bitwise;
     and both equal the oracle on that layer (kernel.py:2011-2061: logical page p
