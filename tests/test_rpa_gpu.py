@@ -327,6 +327,28 @@ def test_nan_cached_kv_stays_in_its_sequence(gpu_device, q_len):
 
 @pytest.mark.parametrize("dt", [BF16, E4M3])
 @pytest.mark.parametrize("q_len", [1, 4])
+def test_nan_cached_kv_does_not_poison_partial_tiles(gpu_device, q_len, dt):
+    """correctness_test.py:731-757: page size 256 and short sequences, so most
+    tiles are partly past a sequence's keys; every cache slot and page no
+    sequence uses holds NaN, and so does every cached K/V page of sequence 1.
+    Only sequence 1's rows may be NaN; the others equal the oracle."""
+    lens = (129, 2048, 8, 7, 257, 259, 8, 511)
+    seqs = [(q_len, k) for k in lens]
+    n = len(seqs)
+    w = W.make_workload(seqs, 8, 2, 128, 256, kv_dtype=dt, seed=50, nan_fill=True,
+                        distribution=[n, n, n], name=f"nan-partial-q{q_len}")
+    S = w.kv_lens.shape[0]
+    pps = w.page_indices.shape[0] // S
+    w.kv_cache[w.page_indices[pps:pps + O.cdiv(lens[1], 256)].long()] = float("nan")
+    _log(f"[rpa-gpu] case {w.name} {dt}")
+    out = _check_dq(w, gpu_device, q_len, w.name)
+    assert torch.isnan(out[q_len:2 * q_len].float()).all()
+    assert torch.isfinite(out[:q_len].float()).all()
+    assert torch.isfinite(out[2 * q_len:].float()).all()
+
+
+@pytest.mark.parametrize("dt", [BF16, E4M3])
+@pytest.mark.parametrize("q_len", [1, 4])
 @pytest.mark.parametrize("d", [128, 256])
 def test_nan_new_kv_stays_in_its_sequence(gpu_device, d, q_len, dt):
     """correctness_test.py:759-790: NaN new keys and values of one short decode

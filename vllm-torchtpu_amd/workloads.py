@@ -130,16 +130,23 @@ def make_workload(seq_lens, num_q_heads, num_kv_heads, head_dim, page_size, *,
         off += cnt
     if nan_fill:
         used = torch.zeros(num_pages, dtype=torch.bool)
-        flat = kv_cache.view(num_pages, page_size, -1)
+        if kv_cache.element_size() == 1:
+            # fp8 tensors take no masked writes: write the NaN byte (0x7F in both
+            # e4m3fn and e5m2) through a byte view.
+            flat = kv_cache.view(torch.uint8).view(num_pages, page_size, -1)
+            nan = 0x7F
+        else:
+            flat = kv_cache.view(num_pages, page_size, -1)
+            nan = float("nan")
         for s, kl in enumerate(kv_lens):
             cnt = cdiv(kl, page_size)
             pages = page_indices[s * pps:s * pps + cnt].long()
             used[pages] = True
             tail = cnt * page_size - kl  # unused rows of the last page
             if tail:
-                flat[pages[-1], page_size - tail:] = float("nan")
+                flat[pages[-1], page_size - tail:] = nan
             page_indices[s * pps + cnt:(s + 1) * pps] = -1
-        flat[~used] = float("nan")
+        flat[~used] = nan
         page_indices[n * pps:] = -1
     cu = torch.zeros(max_num_seqs + 1, dtype=torch.int32)
     cu[1:n + 1] = torch.cumsum(torch.tensor(q_lens, dtype=torch.int64), 0).to(torch.int32)
