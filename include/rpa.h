@@ -116,7 +116,13 @@ typedef struct rpa_desc {
    * 16 / (num_q_heads / num_kv_heads)) run on the decode kernel; the result
    * does not depend on it. */
   int32_t decode_query_size;
-  int32_t reserved[6];
+  /* bool: sliding_window also masks rows without the causal mask (keys
+   * j <= p - sliding_window excluded, p the row's position), as the head_dim-64
+   * reference does (kernel_hd64.py:155-158, :443-446).  0 = the window masks
+   * causal rows only (kernel.py:196-204).  With use_causal_mask = 0 and a
+   * window, such calls run on the shape-generic kernels. */
+  int32_t window_all_rows;
+  int32_t reserved[5];
 } rpa_desc;
 
 /* ABI version compiled into the library. */

@@ -89,12 +89,15 @@ def quantize_q(q: torch.Tensor, q_scale: float, kv_dtype: torch.dtype) -> np.nda
 def brute_force_rpa(q, k, v, kv_cache, kv_lens, page_indices, cu_q_lens, distribution, *,
                     sm_scale=1.0, sliding_window=None, soft_cap=None, k_scale=None,
                     v_scale=None, q_scale=None, use_causal_mask=True, skip_kv_update=False,
-                    return_lse=False, attention_sink=None):
+                    return_lse=False, attention_sink=None, window_all_rows=False):
     """Per-element fp64 attention written directly from the semantic contract
     (positions, page table, K/V combined-head interleave), independent of the
     oracle's gather/einsum code.  Returns [num_tokens, Hq, D] float64 (and,
     with return_lse, the per-row log(sum_j exp(logit_j)) [num_tokens, Hq]).
     attention_sink [Hq]: one more term exp(sink) in each row's denominator.
+    window_all_rows: without the causal mask, keys j <= pos - sliding_window are
+    still excluded (the head_dim 64 contract, kernel_hd64.py:155-158); the v3
+    contract windows causal rows only (kernel.py:196-204).
     q_scale (kernel.py:176-183): q is quantized by `quantize_q` and the logit
     multiplied by q_scale.
     A head_dim 64 packed cache is read through its view
@@ -134,6 +137,9 @@ def brute_force_rpa(q, k, v, kv_cache, kv_lens, page_indices, cu_q_lens, distrib
                         if j > pos:
                             continue
                         if sliding_window is not None and j <= pos - sliding_window:
+                            continue
+                    elif window_all_rows and sliding_window is not None:
+                        if j <= pos - sliding_window:
                             continue
                     x = float(np.dot(Q[q0 + i, gq], kr)) * sm_scale
                     if k_scale is not None:

@@ -115,6 +115,32 @@ def test_hd64_sink_vs_bruteforce(case, dt):
     assert_close(out32, bf, 1e-5, 1e-5, "fp32 mode")
 
 
+@pytest.mark.parametrize("dt", [BF16, E4M3])
+def test_hd64_noncausal_window_vs_bruteforce(dt):
+    """kernel_hd64.py:155-158: without the causal mask the window still drops
+    keys j <= pos - W of every row (future keys stay).  The brute force states
+    that per element; a planted oracle that ignores the window (the v3 rule,
+    kernel.py:196-204) must fail, and W >= kv_len is the unwindowed result."""
+    scales = dict(k_scale=0.75, v_scale=1.5) if dt == E4M3 else {}
+    w = wl64([(7, 20), (1, 9), (5, 5), (12, 40)], 4, 2, 8, kv_dtype=dt, seed=9, **scales)
+    sink = torch.linspace(-1.0, 2.0, 4)
+    kw = dict(w.kwargs)
+    kw.pop("sliding_window", None)
+    out, _ = O.ref_ragged_paged_attention_hd64(*w.args(), sink, mode="fp64",
+                                               use_causal_mask=False, sliding_window=3, **kw)
+    bf = brute_force_rpa(w.q, w.k, w.v, as_view(w.kv_cache), *w.args()[4:], attention_sink=sink,
+                         use_causal_mask=False, sliding_window=3, window_all_rows=True, **kw)
+    assert_close(out, bf, 1e-10, 1e-10, "hd64 non-causal window vs brute force")
+    planted = brute_force_rpa(w.q, w.k, w.v, as_view(w.kv_cache), *w.args()[4:],
+                              attention_sink=sink, use_causal_mask=False, sliding_window=3, **kw)
+    assert (out - planted).abs().max().item() > 1e-3
+    wide, _ = O.ref_ragged_paged_attention_hd64(*w.args(), sink, mode="fp64",
+                                                use_causal_mask=False, sliding_window=40, **kw)
+    none, _ = O.ref_ragged_paged_attention_hd64(*w.args(), sink, mode="fp64",
+                                                use_causal_mask=False, **kw)
+    assert_close(wide, none, 1e-12, 1e-12, "window >= kv_len")
+
+
 def test_sink_closed_form():
     """A sink s scales each row by sigmoid(lse - s) = 1 / (1 + exp(s - lse)),
     lse from the v3 oracle (pinned separately); s = -inf is no sink; a huge s
@@ -225,6 +251,6 @@ def test_hd64_requires_device():
     w = _valid()
     with pytest.raises(RuntimeError, match="no CPU path"):
         R.ragged_paged_attention_hd64(*w.args(), **w.kwargs)
-    with pytest.raises(NotImplementedError):
+    with pytest.raises(RuntimeError, match="no CPU path"):
         R.ragged_paged_attention_hd64(*w.args(), use_causal_mask=False, sliding_window=4,
                                       **w.kwargs)

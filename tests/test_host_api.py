@@ -43,9 +43,10 @@ def test_desc_layout_matches_c():
     #include <stddef.h>
     #include "rpa.h"
     int main(void) {
-      printf("%zu %zu %zu %zu %zu %zu\n", sizeof(rpa_desc), offsetof(rpa_desc, soft_cap),
+      printf("%zu %zu %zu %zu %zu %zu %zu\n", sizeof(rpa_desc), offsetof(rpa_desc, soft_cap),
              offsetof(rpa_desc, sm_scale), offsetof(rpa_desc, path),
-             offsetof(rpa_desc, decode_query_size), offsetof(rpa_desc, reserved));
+             offsetof(rpa_desc, decode_query_size), offsetof(rpa_desc, window_all_rows),
+             offsetof(rpa_desc, reserved));
       return 0;
     }
     """
@@ -57,7 +58,8 @@ def test_desc_layout_matches_c():
         vals = [int(x) for x in subprocess.check_output([exe]).split()]
     D = N.RpaDesc
     assert vals == [__import__("ctypes").sizeof(D), D.soft_cap.offset, D.sm_scale.offset,
-                    D.path.offset, D.decode_query_size.offset, D.reserved.offset]
+                    D.path.offset, D.decode_query_size.offset, D.window_all_rows.offset,
+                    D.reserved.offset]
 
 
 def _desc(**over):

@@ -194,3 +194,14 @@ def test_hd64_backend_with_sinks(gpu_device):
                                                    mode="fp32", **w.kwargs)
     assert_close(out[:n].reshape(n, hq, 64).cpu(), exp_out, 2e-2, 2e-2, "backend hd64")
     assert bytes_equal(g.kv_cache.cpu(), exp_cache)
+
+
+@pytest.mark.parametrize("dt", [BF16, E4M3])
+@pytest.mark.parametrize("window", [3, 64])
+def test_hd64_noncausal_window(gpu_device, window, dt):
+    """kernel_hd64.py:155-158, :443-446: without the causal mask the window
+    still drops keys j <= pos - W of every row (this runs on the generic kernels)."""
+    scales = dict(k_scale=0.75, v_scale=1.25) if dt == E4M3 else {}
+    w = wl64([(1, 700), (40, 300), (1, 5), (17, 17), (3, 90)], 16, 4, 16, "hd64-nc-window",
+             sliding_window=window, kv_dtype=dt, **scales)
+    check(w, gpu_device, _sink(16, 3), use_causal_mask=False)

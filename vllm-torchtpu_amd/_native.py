@@ -94,7 +94,8 @@ class RpaDesc(ctypes.Structure):
         ("v_scale", ctypes.c_float),
         ("path", ctypes.c_int32),
         ("decode_query_size", ctypes.c_int32),
-        ("reserved", ctypes.c_int32 * 6),
+        ("window_all_rows", ctypes.c_int32),
+        ("reserved", ctypes.c_int32 * 5),
     ]
 
 

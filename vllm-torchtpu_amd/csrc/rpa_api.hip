@@ -43,6 +43,7 @@ rpa::Params make_params(const rpa_desc* d) {
   p.pps = d->pages_per_seq;
   p.causal = d->use_causal_mask ? 1 : 0;
   p.window = d->sliding_window > 0 ? d->sliding_window : 0;
+  p.window_nc = (d->window_all_rows && !d->use_causal_mask && p.window > 0) ? 1 : 0;
   p.has_cap = d->has_soft_cap ? 1 : 0;
   p.cap = d->soft_cap;
   p.inv_cap = d->has_soft_cap ? 1.0f / d->soft_cap : 0.0f;
@@ -66,7 +67,8 @@ rpa::Params make_params(const rpa_desc* d) {
 // the shape allows it) followed by the finish kernel; the generic path is the
 // KV-page write followed by the shape-generic attention kernel.
 bool use_fused_path(const rpa_desc* d, const rpa::Params& p) {
-  return d->path != RPA_PATH_GENERIC &&
+  // A window on rows without the causal mask is the generic kernels' only.
+  return d->path != RPA_PATH_GENERIC && !p.window_nc &&
          rpa::finish_supported(p, d->q_dtype, d->kv_dtype, d->out_dtype);
 }
 bool use_decode_kernel(const rpa_desc* d, const rpa::Params& p) {

@@ -26,6 +26,7 @@ struct Params {
   int32_t pps;     // pages_per_seq
   int32_t causal;  // use_causal_mask
   int32_t window;  // sliding_window, <= 0 = none
+  int32_t window_nc;  // the window also masks rows without the causal mask
   int32_t has_cap;
   float cap;
   float inv_cap;

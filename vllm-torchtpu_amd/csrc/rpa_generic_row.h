@@ -5,7 +5,8 @@
 //   s_j = (q_g . k_{g/qpk, j}) * sm_scale * k_scale * q_scale,
 //   s_j = cap * tanh(s_j / cap)                 (soft cap, kernel.py:193-194)
 //   keys with j > p, or j <= p - W under a window, are excluded
-//   (causal mask kernel.py:196-204)
+//   (causal mask kernel.py:196-204); without the causal mask, a window with
+//   window_nc set excludes j <= p - W alone (kernel_hd64.py:155-158)
 //   out = softmax(s) . v * v_scale               (kernel.py:205-209)
 // Masked keys get weight exactly 0 (mask_value = finfo.min underflows).
 //
@@ -67,6 +68,8 @@ __device__ __forceinline__ void generic_row(const Params& p, const float* qs,
   if (p.causal) {
     hi = min(kv_len, pos + 1);
     if (p.window > 0) lo = max(0, pos - p.window + 1);
+  } else if (p.window_nc) {
+    lo = max(0, pos - p.window + 1);  // kernel_hd64.py:155-158: window without causality
   }
   const int32_t h = g / p.qpk;
   const int32_t new_start = kv_len - q_len;

@@ -230,7 +230,8 @@ def dynamic_validate_inputs(queries, keys, values, kv_cache, kv_lens, page_indic
 # ---------------------------------------------------------------------------
 def _make_desc(q, k, kv_cache, kv_lens, page_indices, out_dtype, *, use_causal_mask,
                skip_kv_update, sm_scale, sliding_window, soft_cap, q_scale, k_scale,
-               v_scale, path=N.RPA_PATH_AUTO, decode_query_size=1) -> N.RpaDesc:
+               v_scale, path=N.RPA_PATH_AUTO, decode_query_size=1,
+               window_all_rows=False) -> N.RpaDesc:
     d = N.RpaDesc()
     d.abi_version = N.ABI_VERSION
     d.q_dtype = N.rpa_dtype(q.dtype)
@@ -258,6 +259,7 @@ def _make_desc(q, k, kv_cache, kv_lens, page_indices, out_dtype, *, use_causal_m
     d.v_scale = 1.0 if v_scale is None else float(v_scale)
     d.path = int(path)
     d.decode_query_size = int(decode_query_size)
+    d.window_all_rows = int(bool(window_all_rows))
     return d
 
 
@@ -325,7 +327,7 @@ def _rpa_forward_impl(queries, keys, values, kv_cache, kv_lens, page_indices, cu
                       distribution, out, *, use_causal_mask, skip_kv_update, sm_scale,
                       sliding_window, soft_cap, q_scale, k_scale, v_scale,
                       path=N.RPA_PATH_AUTO, workspace=None, lse=None, attention_sink=None,
-                      decode_query_size=1):
+                      decode_query_size=1, window_all_rows=False):
     L = N.lib()
     _require_device(queries, keys, values, kv_cache, kv_lens, page_indices, cu_q_lens,
                     distribution, out)
@@ -339,7 +341,7 @@ def _rpa_forward_impl(queries, keys, values, kv_cache, kv_lens, page_indices, cu
                       use_causal_mask=use_causal_mask, skip_kv_update=skip_kv_update,
                       sm_scale=sm_scale, sliding_window=sliding_window, soft_cap=soft_cap,
                       q_scale=q_scale, k_scale=k_scale, v_scale=v_scale, path=path,
-                      decode_query_size=decode_query_size)
+                      decode_query_size=decode_query_size, window_all_rows=window_all_rows)
     N.check(L.rpa_validate_desc(desc), "rpa_validate_desc")
     if desc.max_num_seqs > MAX_FAST_SEQS and desc.max_num_seqs not in _WARNED_GENERIC:
         _WARNED_GENERIC.add(desc.max_num_seqs)

@@ -16,7 +16,9 @@ Deliberate differences (besides those of rpa.py):
     strictly, as the reference function (ref_ragged_paged_attention_hd64)
     does, whatever the flag says.
   * The block-size knobs are validated and otherwise ignored.
-  * sliding_window with use_causal_mask=False raises NotImplementedError.
+  * sliding_window with use_causal_mask=False masks keys j <= p - W of every
+    row, as kernel_hd64.py:155-158 and :443-446 do (the v3 reference windows
+    causal rows only); such calls run on the shape-generic kernels.
 """
 
 from __future__ import annotations
@@ -196,7 +198,7 @@ def _rpa_hd64_op(queries: torch.Tensor, keys: torch.Tensor, values: torch.Tensor
         distribution, out, use_causal_mask=use_causal_mask, skip_kv_update=skip_kv_update,
         sm_scale=sm_scale, sliding_window=sliding_window if sliding_window > 0 else None,
         soft_cap=soft_cap if has_soft_cap else None, q_scale=q_scale, k_scale=k_scale,
-        v_scale=v_scale, attention_sink=attention_sink)
+        v_scale=v_scale, attention_sink=attention_sink, window_all_rows=True)
 
 
 @_rpa_hd64_op.register_fake
@@ -248,10 +250,6 @@ def ragged_paged_attention_hd64(
     if mask_value is not None and mask_value > -1e30:
         raise NotImplementedError(
             f"{mask_value=}: only mask values <= -1e30 (the default) are supported")
-    if sliding_window is not None and not use_causal_mask:
-        # kernel_hd64.py:443-446 masks the window without the causal mask too;
-        # the HIP kernels window only causal rows.
-        raise NotImplementedError("sliding_window without use_causal_mask")
     _require_device(queries, keys, values, kv_cache)
     q = queries
     if q_scale is not None:  # kernel_hd64.py:126-133
