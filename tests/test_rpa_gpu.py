@@ -472,6 +472,32 @@ def test_decode_repeated_calls(gpu_device):
     check(W.make_workload(DECODE_EDGE, 32, 8, 128, 16, seed=37, name="decode-after"), gpu_device)
 
 
+def test_back_to_back_calls_without_sync(gpu_device):
+    """Calls queued on one stream with no synchronization between them share the
+    device's workspace (decode partials and plan): call i's merges must read call
+    i's partials, not those of call i + 1 that the next decode kernel writes.
+    Two decode batches and a mixed batch take turns nine times, then every
+    output is checked."""
+    a = W.make_workload([(1, k) for k in (4000, 33, 2048, 700, 1)], 32, 8, 128, 16, seed=38,
+                        name="b2b-a")
+    b = W.make_workload([(1, k) for k in (1500, 3000, 64, 900, 2500)], 32, 8, 128, 16,
+                        seed=39, name="b2b-b")
+    c = W.make_workload([(1, 800), (37, 120), (1, 2000), (64, 64)], 32, 8, 128, 16, seed=40,
+                        name="b2b-mixed")
+    ws = [a, b, c]
+    exp = {w.name: O.ref_ragged_paged_attention(*w.args(), mode="fp32", **w.kwargs)[0]
+           for w in ws}
+    gs = [w.to(gpu_device) for w in ws]
+    torch.cuda.synchronize()
+    outs = []
+    for rep in range(9):
+        w, g = ws[rep % 3], gs[rep % 3]
+        outs.append((w, R.ragged_paged_attention(*g.args(), **w.kwargs)[0]))
+    torch.cuda.synchronize()
+    for rep, (w, out) in enumerate(outs):
+        assert_close(out[:w.num_tokens].cpu(), exp[w.name], 2e-2, 2e-2, f"{w.name} call {rep}")
+
+
 def test_decode_one_pair_many_partials(gpu_device):
     """One long decode pair spread over nearly every decode wavefront (about 900
     partials): the merge combines them 64 units at a time (rpa_merge.h)."""
