@@ -118,6 +118,26 @@ def test_mask_value_policy():
         R.ragged_paged_attention(*w.args(), mask_value=-1.0, **w.kwargs)
 
 
+def test_static_validation_memo_keeps_errors():
+    """A signature that passed validation is remembered; a failing one is not, and
+    any argument the rules read (a dtype, a window) makes a new signature."""
+    w = R.workloads.make_workload([(3, 20), (1, 9)], 8, 2, 128, 16, seed=0)
+    for _ in range(2):
+        with pytest.raises(RuntimeError, match="no CPU path"):
+            R.ragged_paged_attention(*w.args(), **w.kwargs)
+    for _ in range(2):
+        with pytest.raises(ValueError):
+            R.ragged_paged_attention(*w.args(), sliding_window=0, **w.kwargs)
+    args = list(w.args())
+    args[4] = args[4].to(torch.int64)
+    for _ in range(2):
+        with pytest.raises(ValueError, match="int32"):
+            R.ragged_paged_attention(*args, **w.kwargs)
+    with pytest.raises(ValueError):
+        R.ragged_paged_attention(*w.args(), use_causal_mask=True, skip_kv_mask=True,
+                                 **w.kwargs)
+
+
 def test_custom_op_fake_shape():
     from torch._subclasses.fake_tensor import FakeTensorMode
     w = R.workloads.make_workload([(3, 20), (1, 9)], 8, 2, 128, 16, seed=0)

@@ -498,6 +498,36 @@ def test_back_to_back_calls_without_sync(gpu_device):
         assert_close(out[:w.num_tokens].cpu(), exp[w.name], 2e-2, 2e-2, f"{w.name} call {rep}")
 
 
+def test_custom_op_path_matches_eager_path(gpu_device):
+    """Eager calls run the custom op's body directly; the registered ops (the path
+    torch.compile keeps opaque) must give the same bytes, with and without out=
+    and return_lse."""
+    w = W.make_workload([(1, 800), (37, 120), (1, 2000), (64, 64)], 16, 4, 128, 16, seed=41,
+                        name="op-path")
+    g = w.to(gpu_device)
+    kw = w.kwargs
+    out_e, _ = R.ragged_paged_attention(*g.args(), **kw)
+    out_o = torch.ops.rpa_amd.ragged_paged_attention(
+        *g.args(), g.q.dtype, True, False, float(kw["sm_scale"]), 0, 0.0, False, 1.0, 1.0, 1.0,
+        N.RPA_PATH_AUTO, 1)
+    buf = torch.empty_like(g.q)
+    torch.ops.rpa_amd.ragged_paged_attention_out(
+        *g.args(), buf, True, False, float(kw["sm_scale"]), 0, 0.0, False, 1.0, 1.0, 1.0,
+        N.RPA_PATH_AUTO, 1)
+    out_l, _, lse_e = R.ragged_paged_attention(*g.args(), return_lse=True, **kw)
+    out_lo, lse_o = torch.ops.rpa_amd.ragged_paged_attention_lse(
+        *g.args(), g.q.dtype, True, False, float(kw["sm_scale"]), 0, 0.0, False, 1.0, 1.0, 1.0,
+        N.RPA_PATH_AUTO, 1)
+    torch.cuda.synchronize()
+    n = w.num_tokens
+    assert torch.equal(out_e[:n].view(torch.int16), out_o[:n].view(torch.int16))
+    assert torch.equal(out_e[:n].view(torch.int16), buf[:n].view(torch.int16))
+    assert torch.equal(out_l[:n].view(torch.int16), out_lo[:n].view(torch.int16))
+    assert torch.equal(lse_e[:n], lse_o[:n])
+    exp = O.ref_ragged_paged_attention(*w.args(), mode="fp32", **kw)[0]
+    assert_close(out_e[:n].cpu(), exp, 2e-2, 2e-2, "op-path")
+
+
 def test_decode_one_pair_many_partials(gpu_device):
     """One long decode pair spread over nearly every decode wavefront (about 900
     partials): the merge combines them 64 units at a time (rpa_merge.h)."""
