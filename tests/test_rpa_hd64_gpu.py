@@ -205,3 +205,17 @@ def test_hd64_noncausal_window(gpu_device, window, dt):
     w = wl64([(1, 700), (40, 300), (1, 5), (17, 17), (3, 90)], 16, 4, 16, "hd64-nc-window",
              sliding_window=window, kv_dtype=dt, **scales)
     check(w, gpu_device, _sink(16, 3), use_causal_mask=False)
+
+
+def test_hd64_custom_op_matches_eager(gpu_device):
+    """Eager hd64 calls run the op body directly; the registered op (the path
+    torch.compile keeps opaque) must give the same bytes."""
+    w = wl64([(1, 700), (40, 300), (1, 5)], 16, 4, 16, "hd64-op", sliding_window=64)
+    g = w.to(gpu_device)
+    sink = _sink(16, 4).to(gpu_device)
+    out_e, _ = R.ragged_paged_attention_hd64(*g.args(), sink, **w.kwargs)
+    out_o = torch.ops.rpa_amd.ragged_paged_attention_hd64(
+        *g.args(), sink, True, False, float(w.kwargs["sm_scale"]), 64, 0.0, False, 1.0, 1.0, 1.0)
+    torch.cuda.synchronize()
+    n = w.num_tokens
+    assert torch.equal(out_e[:n].view(torch.int16), out_o[:n].view(torch.int16))

@@ -184,6 +184,22 @@ def _as_head_packed(kv_cache: torch.Tensor) -> torch.Tensor:
     return kv_cache.view(p, ps, 2 * hp, pack, 64)
 
 
+def _rpa_hd64_impl(queries: torch.Tensor, keys: torch.Tensor, values: torch.Tensor,
+                   kv_cache: torch.Tensor, kv_lens: torch.Tensor, page_indices: torch.Tensor,
+                   cu_q_lens: torch.Tensor, distribution: torch.Tensor,
+                   attention_sink: torch.Tensor | None, use_causal_mask: bool,
+                   skip_kv_update: bool, sm_scale: float, sliding_window: int, soft_cap: float,
+                   has_soft_cap: bool, q_scale: float, k_scale: float,
+                   v_scale: float) -> torch.Tensor:
+    out = torch.empty(queries.shape, dtype=queries.dtype, device=queries.device)
+    return _rpa_forward_impl(
+        queries, keys, values, _as_head_packed(kv_cache), kv_lens, page_indices, cu_q_lens,
+        distribution, out, use_causal_mask=use_causal_mask, skip_kv_update=skip_kv_update,
+        sm_scale=sm_scale, sliding_window=sliding_window if sliding_window > 0 else None,
+        soft_cap=soft_cap if has_soft_cap else None, q_scale=q_scale, k_scale=k_scale,
+        v_scale=v_scale, attention_sink=attention_sink, window_all_rows=True)
+
+
 @torch.library.custom_op("rpa_amd::ragged_paged_attention_hd64", mutates_args=("kv_cache",))
 def _rpa_hd64_op(queries: torch.Tensor, keys: torch.Tensor, values: torch.Tensor,
                  kv_cache: torch.Tensor, kv_lens: torch.Tensor, page_indices: torch.Tensor,
@@ -192,13 +208,10 @@ def _rpa_hd64_op(queries: torch.Tensor, keys: torch.Tensor, values: torch.Tensor
                  skip_kv_update: bool, sm_scale: float, sliding_window: int, soft_cap: float,
                  has_soft_cap: bool, q_scale: float, k_scale: float,
                  v_scale: float) -> torch.Tensor:
-    out = torch.empty(queries.shape, dtype=queries.dtype, device=queries.device)
-    return _rpa_forward_impl(
-        queries, keys, values, _as_head_packed(kv_cache), kv_lens, page_indices, cu_q_lens,
-        distribution, out, use_causal_mask=use_causal_mask, skip_kv_update=skip_kv_update,
-        sm_scale=sm_scale, sliding_window=sliding_window if sliding_window > 0 else None,
-        soft_cap=soft_cap if has_soft_cap else None, q_scale=q_scale, k_scale=k_scale,
-        v_scale=v_scale, attention_sink=attention_sink, window_all_rows=True)
+    return _rpa_hd64_impl(queries, keys, values, kv_cache, kv_lens, page_indices, cu_q_lens,
+                          distribution, attention_sink, use_causal_mask, skip_kv_update,
+                          sm_scale, sliding_window, soft_cap, has_soft_cap, q_scale, k_scale,
+                          v_scale)
 
 
 @_rpa_hd64_op.register_fake
@@ -256,6 +269,17 @@ def ragged_paged_attention_hd64(
         info = torch.finfo(kv_cache.dtype)
         q = torch.clamp(q / q_scale, min=info.min, max=info.max).to(kv_cache.dtype)
     sink = None if attention_sink is None else attention_sink.contiguous()
+    if type(queries) is torch.Tensor and not torch.compiler.is_compiling():
+        # Eager call on real tensors: the op's body without its dispatcher.
+        out = _rpa_hd64_impl(
+            q.contiguous(), keys.contiguous(), values.contiguous(), kv_cache, kv_lens,
+            page_indices, cu_q_lens, distribution, sink, bool(use_causal_mask),
+            bool(skip_kv_update), float(sm_scale),
+            0 if sliding_window is None else int(sliding_window),
+            0.0 if soft_cap is None else float(soft_cap), soft_cap is not None,
+            1.0 if q_scale is None else float(q_scale), 1.0 if k_scale is None else float(k_scale),
+            1.0 if v_scale is None else float(v_scale))
+        return out, kv_cache
     out = torch.ops.rpa_amd.ragged_paged_attention_hd64(
         q.contiguous(), keys.contiguous(), values.contiguous(), kv_cache, kv_lens, page_indices,
         cu_q_lens, distribution, sink, bool(use_causal_mask), bool(skip_kv_update),
